@@ -1,0 +1,123 @@
+/* turbopress_amd: MI355X (gfx950) kernels for TurboPress's packed-TCQ decode path.
+ *
+ * C ABI of libturbopress_amd.so.  Every entry point takes plain device
+ * pointers, sizes in elements or bytes, and a hipStream_t passed as void*.
+ * None allocates memory, none synchronises the host, and none autotunes, so
+ * all device entry points may be recorded into a HIP graph.  All return an
+ * int status (TP_OK == 0); tp_status_string() names it.
+ *
+ * Data formats follow the reference's format v2 (turbopress/runtime.py:73-100,
+ * 171-186): fp16 values are passed as raw uint16 bit patterns, packed streams
+ * are little-endian bit streams with each row padded to whole bytes.
+ *
+ * Reference paths below are relative to the TurboPress 0.5.2 checkout.
+ */
+#ifndef TURBOPRESS_AMD_H
+#define TURBOPRESS_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TP_ABI_VERSION 1
+
+enum tp_status {
+  TP_OK = 0,
+  TP_ERR_NULL_POINTER = 1,        /* a required pointer is NULL */
+  TP_ERR_UNSUPPORTED_BITS = 2,    /* bits outside what the entry point supports */
+  TP_ERR_UNSUPPORTED_STATES = 3,  /* n_states not in {4, 8, 16, 64} */
+  TP_ERR_BAD_DIMS = 4,            /* non-positive or inconsistent sizes */
+  TP_ERR_MISALIGNED = 5,          /* pointer or stride alignment violated */
+  TP_ERR_BAD_BLOCK = 6,           /* Hadamard block not a power of 2 dividing d, or too large */
+  TP_ERR_HIP = 7,                 /* a HIP launch or query failed */
+  TP_ERR_WORKSPACE = 8,           /* workspace missing or too small */
+  TP_ERR_BAD_LAYOUT = 9           /* device-layout descriptor inconsistent with the call */
+};
+
+/* ABI version of the loaded library (TP_ABI_VERSION when headers match). */
+int tp_abi_version(void);
+
+/* Static, human-readable name of a status code. */
+const char* tp_status_string(int status);
+
+/* ---------------------------------------------------------------------------
+ * Trellis tables (host only, no GPU work)
+ * ------------------------------------------------------------------------- */
+
+/* Window -> subset LUT of the S-state trellis, lut_len >= 2*S entries.
+ * Replaces turbopress/runtime.py:106-119 (subset_lut) over
+ * turbopress/trellis.py:64-80 (Trellis.subset_table). */
+int tp_subset_lut(int n_states, uint8_t* lut_out, int lut_len);
+
+/* ---------------------------------------------------------------------------
+ * Rotation
+ * ------------------------------------------------------------------------- */
+
+/* z = blockFWHT(x * rot_scale): orthonormal Sylvester Walsh-Hadamard transform
+ * applied independently to each contiguous `block` of the last dimension,
+ * computed in fp32 and stored as fp16.  x, z: fp16 [batch, d] row-major
+ * (z may not alias x); rot_scale: fp16 [d].  block must be a power of 2
+ * dividing d, at most 16384.
+ * Replaces turbopress/triton_kernel.py:235-260 (fwht_scale); the math is
+ * turbopress/runtime.py:192-208 and turbopress/hadamard.py:37-56. */
+int tp_fwht_scale(const uint16_t* x, const uint16_t* rot_scale, uint16_t* z,
+                  int64_t batch, int64_t d, int64_t block, void* stream);
+
+/* out = blockFWHT(x * pre_scale) * post_scale over `rows` rows of length d
+ * (either scale may be NULL), fp32 butterflies, fp16 in/out.  With
+ * pre_scale = NULL and post_scale = rot_scale this is the load-time fold of
+ * decoded rotated weights back to the original basis,
+ * turbopress/runtime.py:282-286 (mode "cached"); with post_scale = NULL it is
+ * tp_fwht_scale. */
+int tp_block_fwht_rows(const uint16_t* x, const uint16_t* pre_scale,
+                       const uint16_t* post_scale, uint16_t* out,
+                       int64_t rows, int64_t d, int64_t block, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Decode (natural format v2 streams)
+ * ------------------------------------------------------------------------- */
+
+/* levels[r, c] = member[r, c] * 4 + LUT[window(r, c)] for n_rows rows, as
+ * uint8 [n_rows, out_stride].  path: [n_rows, path_stride] bytes (1 bit per
+ * weight); member: [n_rows, member_stride] bytes ((bits-1) bits per weight),
+ * or NULL when bits == 1.  bits in [1, 7].
+ * Replaces turbopress/runtime.py:122-139 (window_decode_levels) applied to
+ * turbopress/runtime.py:93-100 (unpack_le) of the packed streams. */
+int tp_window_decode_levels(const uint8_t* path, int64_t path_stride,
+                            const uint8_t* member, int64_t member_stride,
+                            int64_t n_rows, int64_t d, int bits, int n_states,
+                            uint8_t* levels_out, int64_t out_stride, void* stream);
+
+/* w[r, c] = fp16(f32(codebook[level[r, c]]) * f32(scales[r])), the rotated
+ * weight rows of a packed linear, fp16 [n_rows, out_stride].  The pointers
+ * address the first row to decode (a row slice is a pointer offset).
+ * Replaces turbopress/runtime.py:291-301 (PackedTCQLinear.decode_rows). */
+int tp_decode_rows(const uint8_t* path, int64_t path_stride,
+                   const uint8_t* member, int64_t member_stride,
+                   const uint16_t* scales, const uint16_t* codebook,
+                   int64_t n_rows, int64_t d, int bits, int n_states,
+                   uint16_t* w_out, int64_t out_stride, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * GEMV on natural format v2 streams (any bits in [1, 7], any S, any batch)
+ * ------------------------------------------------------------------------- */
+
+/* y[b, r] = fp16(scale[r] * sum_c codebook[level[r, c]] * z[b, c]) (+ bias[r]
+ * added in fp16 as the reference does), fp32 accumulation.  z: fp16 [batch, d]
+ * rotated activations; y: fp16 [batch, n]; bias may be NULL.
+ * Replaces turbopress/triton_kernel.py:132-157 (packed_gemv) followed by
+ * turbopress/runtime.py:332-333 (bias). */
+int tp_tcq_gemv(const uint16_t* z, int64_t batch,
+                const uint8_t* path, int64_t path_stride,
+                const uint8_t* member, int64_t member_stride,
+                const uint16_t* scales, const uint16_t* codebook, const uint16_t* bias,
+                int64_t n, int64_t d, int bits, int n_states,
+                uint16_t* y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TURBOPRESS_AMD_H */

@@ -1,0 +1,81 @@
+"""The C-ABI library loads, exports every declared symbol, and validates
+arguments on the host (CPU only: no call here reaches the GPU)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(tp_[a-z0-9_]+)\s*\(", text))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = _declared_symbols()
+    for required in ("tp_abi_version", "tp_fwht_scale", "tp_decode_rows",
+                     "tp_window_decode_levels", "tp_tcq_gemv", "tp_subset_lut"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(built_lib):
+    for name in _declared_symbols():
+        assert hasattr(built_lib, name), name
+
+
+def test_ctypes_table_covers_header():
+    from turbopress_amd import _lib
+    assert set(_lib.SIGNATURES) == set(_declared_symbols())
+
+
+def test_abi_version_and_status_strings(built_lib):
+    from turbopress_amd import _lib
+    assert built_lib.tp_abi_version() == _lib.ABI_VERSION
+    for code in range(10):
+        assert _lib.status_string(code) != "unknown status"
+    assert _lib.status_string(99) == "unknown status"
+
+
+@pytest.mark.parametrize("n_states", [4, 8, 16, 64])
+def test_subset_lut_host_function_matches_oracle(built_lib, n_states):
+    from oracle.tcq_oracle import subset_lut
+    buf = (ctypes.c_uint8 * (2 * n_states))()
+    assert built_lib.tp_subset_lut(n_states, buf, 2 * n_states) == 0
+    assert np.array_equal(np.frombuffer(bytes(buf), dtype=np.uint8), subset_lut(n_states))
+
+
+def test_host_side_argument_validation(built_lib):
+    from turbopress_amd import _lib
+    buf = (ctypes.c_uint8 * 256)()
+    assert built_lib.tp_subset_lut(6, buf, 256) == _lib.TP_ERR_UNSUPPORTED_STATES
+    assert built_lib.tp_subset_lut(64, buf, 64) == _lib.TP_ERR_BAD_DIMS
+    # Null pointers, bad block and bad bits are rejected before any GPU call.
+    assert built_lib.tp_fwht_scale(None, None, None, 1, 64, 64, None) == _lib.TP_ERR_NULL_POINTER
+    fake = ctypes.c_void_p(16)
+    assert built_lib.tp_fwht_scale(fake, fake, fake, 1, 96, 64, None) == _lib.TP_ERR_BAD_BLOCK
+    assert built_lib.tp_fwht_scale(fake, fake, fake, 1, 96, 48, None) == _lib.TP_ERR_BAD_BLOCK
+    assert built_lib.tp_decode_rows(fake, 12, fake, 24, fake, fake, 4, 96, 9, 64, fake, 96, None) \
+        == _lib.TP_ERR_UNSUPPORTED_BITS
+    assert built_lib.tp_decode_rows(fake, 12, fake, 24, fake, fake, 4, 96, 3, 32, fake, 96, None) \
+        == _lib.TP_ERR_UNSUPPORTED_STATES
+    assert built_lib.tp_decode_rows(fake, 11, fake, 24, fake, fake, 4, 96, 3, 64, fake, 96, None) \
+        == _lib.TP_ERR_BAD_DIMS
+    assert built_lib.tp_tcq_gemv(fake, 1, fake, 12, None, 24, fake, fake, None, 4, 96, 3, 64,
+                                 fake, None) == _lib.TP_ERR_NULL_POINTER
+
+
+def test_check_maps_status_to_reference_exceptions():
+    from turbopress_amd import _lib
+    with pytest.raises(ValueError):
+        _lib.check(_lib.TP_ERR_BAD_DIMS, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.TP_ERR_HIP, "x")
+    _lib.check(_lib.TP_OK, "x")

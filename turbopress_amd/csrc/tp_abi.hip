@@ -1,0 +1,38 @@
+// Host-only entry points of the C ABI: version, status names, trellis LUT.
+#include "tp_common.h"
+
+extern "C" int tp_abi_version(void) { return TP_ABI_VERSION; }
+
+extern "C" const char* tp_status_string(int status) {
+  switch (status) {
+    case TP_OK: return "ok";
+    case TP_ERR_NULL_POINTER: return "null pointer";
+    case TP_ERR_UNSUPPORTED_BITS: return "unsupported bits per weight";
+    case TP_ERR_UNSUPPORTED_STATES: return "unsupported trellis state count (need 4, 8, 16 or 64)";
+    case TP_ERR_BAD_DIMS: return "bad dimensions";
+    case TP_ERR_MISALIGNED: return "misaligned pointer or stride";
+    case TP_ERR_BAD_BLOCK: return "bad Hadamard block (power of 2 dividing d, at most 16384)";
+    case TP_ERR_HIP: return "HIP launch or runtime error";
+    case TP_ERR_WORKSPACE: return "workspace missing or too small";
+    case TP_ERR_BAD_LAYOUT: return "device layout does not match the call";
+    default: return "unknown status";
+  }
+}
+
+// subset_lut (runtime.py:106-119): LUT[x] = subset of the window x, computed
+// from the window-coordinate generators (same function as the reference's
+// reindexed subset_table lookup).
+extern "C" int tp_subset_lut(int n_states, uint8_t* lut_out, int lut_len) {
+  tp::TrellisTaps t;
+  int st = tp::trellis_taps(n_states, &t);
+  if (st) return st;
+  if (!lut_out) return TP_ERR_NULL_POINTER;
+  const int size = 1 << (t.m + 1);
+  if (lut_len < size) return TP_ERR_BAD_DIMS;
+  for (int x = 0; x < size; ++x) {
+    uint32_t b0 = __builtin_popcount((uint32_t)x & t.g0w) & 1u;
+    uint32_t b1 = __builtin_popcount((uint32_t)x & t.g1w) & 1u;
+    lut_out[x] = (uint8_t)((b1 << 1) | b0);
+  }
+  return TP_OK;
+}

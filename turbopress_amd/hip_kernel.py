@@ -1,0 +1,129 @@
+"""Torch-facing wrappers of the HIP kernels (the reference's triton_kernel.py API).
+
+``HAS_HIP``, ``fwht_scale(x, rot_scale, block)`` and ``packed_gemv(z, layer)``
+keep the names, arguments and error behaviour of
+turbopress/triton_kernel.py:19-27, 132-157, 235-260.  Each call launches
+hand-written HIP kernels from libturbopress_amd.so on torch's current stream;
+nothing here computes on the CPU, and nothing synchronises the host, so the
+calls can be captured in a HIP graph.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from turbopress_amd import _lib
+
+__all__ = ["HAS_HIP", "fwht_scale", "packed_gemv", "decode_rows", "window_decode_levels",
+           "subset_lut", "current_stream_ptr"]
+
+
+def _has_hip() -> bool:
+    try:
+        return _lib.available() and torch.cuda.is_available()
+    except Exception:  # pragma: no cover - defensive: a broken ROCm install
+        return False
+
+
+HAS_HIP: bool = _has_hip()
+
+
+def current_stream_ptr(device: torch.device | None = None) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_cuda(t: Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA (ROCm) tensor; turbopress_amd has no CPU path")
+
+
+def subset_lut(n_states: int) -> Tensor:
+    """uint8 [2*S] window -> subset LUT (runtime.py:106-119), from the C library."""
+    import ctypes
+    size = 2 * n_states
+    buf = (ctypes.c_uint8 * max(size, 1))()
+    _lib.check(_lib.lib().tp_subset_lut(n_states, buf, size), "subset_lut")
+    return torch.tensor(list(buf), dtype=torch.uint8)
+
+
+def fwht_scale(x: Tensor, rot_scale: Tensor, block: int) -> Tensor:
+    """``blockFWHT(x * rot_scale)`` in one HIP launch (triton_kernel.py:235-260).
+
+    fp32 butterflies, fp16 result; x may be any float dtype (cast to fp16 as the
+    reference does, triton_kernel.py:244)."""
+    _require_cuda(x, "x")
+    d = x.shape[-1]
+    flat = x.reshape(-1, d).to(torch.float16).contiguous()
+    rs = rot_scale.to(device=x.device, dtype=torch.float16).contiguous()
+    if rs.numel() != d:
+        raise ValueError(f"rot_scale has {rs.numel()} entries, expected {d}")
+    out = torch.empty_like(flat)
+    st = _lib.lib().tp_fwht_scale(flat.data_ptr(), rs.data_ptr(), out.data_ptr(),
+                                  flat.shape[0], d, int(block), current_stream_ptr(x.device))
+    _lib.check(st, "fwht_scale")
+    return out.reshape(x.shape)
+
+
+def window_decode_levels(path_packed: Tensor, member_packed: Tensor | None, d: int,
+                         bits: int, n_states: int) -> Tensor:
+    """uint8 level codes [n, d] straight from the packed v2 streams
+    (runtime.py:122-139 after unpack_le, runtime.py:93-100)."""
+    _require_cuda(path_packed, "path_packed")
+    path = path_packed.contiguous()
+    n = path.shape[0]
+    mem = None if member_packed is None else member_packed.contiguous()
+    out = torch.empty(n, d, dtype=torch.uint8, device=path.device)
+    st = _lib.lib().tp_window_decode_levels(
+        path.data_ptr(), path.shape[1], 0 if mem is None else mem.data_ptr(),
+        0 if mem is None else mem.shape[1], n, d, bits, n_states, out.data_ptr(), d,
+        current_stream_ptr(path.device))
+    _lib.check(st, "window_decode_levels")
+    return out
+
+
+def decode_rows(layer, r0: int, r1: int) -> Tensor:
+    """fp16 rotated weight rows [r0, r1) of a packed layer (runtime.py:291-301)."""
+    path = layer.path_packed
+    if path is None:
+        raise RuntimeError("layer no longer holds its packed streams")
+    _require_cuda(path, "path_packed")
+    d = layer.in_features
+    r0, r1 = max(0, r0), min(layer.out_features, r1)
+    out = torch.empty(max(r1 - r0, 0), d, dtype=torch.float16, device=path.device)
+    if r1 <= r0:
+        return out
+    mem = layer.member_packed
+    ps = path.stride(0)
+    ms = 0 if mem is None else mem.stride(0)
+    st = _lib.lib().tp_decode_rows(
+        path.data_ptr() + r0 * ps, ps,
+        0 if mem is None else mem.data_ptr() + r0 * ms, ms,
+        layer.scales.data_ptr() + 2 * r0, layer.codebook.data_ptr(),
+        r1 - r0, d, layer.bits, layer.n_states, out.data_ptr(), d,
+        current_stream_ptr(path.device))
+    _lib.check(st, "decode_rows")
+    return out
+
+
+def packed_gemv(z: Tensor, layer, bias: Tensor | None = None) -> Tensor:
+    """y = z @ W_packed^T (+ bias) for a packed layer (triton_kernel.py:132-157).
+
+    ``layer`` is duck-typed: ``in_features``, ``out_features``, ``bits``,
+    ``n_states``, ``scales``, ``codebook`` and the packed streams
+    ``path_packed``/``member_packed``.  Returns fp16 [..., n]."""
+    _require_cuda(z, "z")
+    if getattr(layer, "path_packed", None) is None:
+        raise RuntimeError("layer was not built with mode='hip'")
+    n, d = layer.out_features, layer.in_features
+    flat = z.reshape(-1, d).to(torch.float16).contiguous()
+    out = torch.empty(flat.shape[0], n, dtype=torch.float16, device=z.device)
+    path, mem = layer.path_packed, layer.member_packed
+    st = _lib.lib().tp_tcq_gemv(
+        flat.data_ptr(), flat.shape[0], path.data_ptr(), path.stride(0),
+        0 if mem is None else mem.data_ptr(), 0 if mem is None else mem.stride(0),
+        layer.scales.data_ptr(), layer.codebook.data_ptr(),
+        0 if bias is None else bias.data_ptr(),
+        n, d, layer.bits, layer.n_states, out.data_ptr(), current_stream_ptr(z.device))
+    _lib.check(st, "packed_gemv")
+    return out.reshape(*z.shape[:-1], n)

@@ -1,0 +1,111 @@
+"""Seeded synthetic packed linears and activations for tests and benchmarks.
+
+Every stream the decode path reads is drawn from a CPU ``torch.Generator``
+seeded per linear, in a fixed order:
+
+  1. ``path_packed``   uint8 [n, ceil(d/8)]        uniform bytes
+  2. ``member_packed`` uint8 [n, ceil(d(k-1)/8)]   uniform bytes (k > 1)
+  3. ``scales``        fp16(|N(0, 0.02)| + 1e-3)    [n]
+  4. equilibration     s ~ LogNormal(0, 0.25), ``inv_equil = fp16(1/fp16(s))`` [d]
+  5. signs             Rademacher [d], packed little-endian like ``signs_packed``
+  6. ``bias``          fp16 N(0, 0.1) [n] (only when requested)
+
+Uniform bytes are legal trellis streams: every path bit sequence is a valid
+path of the bitshift trellis and every member code is in range, so they are
+what an encoder could have written.  Padding bits past the last weight of a
+row are zeroed, as ``pack_le`` leaves them (runtime.py:84-90).  The codebook
+is the reference's data-free trellis codebook for (k, S), seed 0.
+
+The result is a format-v2 payload (runtime.py:171-186) that
+``PackedTCQLinear`` accepts unchanged.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from turbopress_amd.codebooks import default_codebook
+
+# Qwen3 decoder-layer projection shapes (in_features -> out_features).
+QWEN3_0_6B_LAYER = {
+    "q_proj": (1024, 2048), "k_proj": (1024, 1024), "v_proj": (1024, 1024),
+    "o_proj": (2048, 1024), "gate_proj": (1024, 3072), "up_proj": (1024, 3072),
+    "down_proj": (3072, 1024),
+}
+QWEN3_4B_LAYER = {
+    "q_proj": (2560, 4096), "k_proj": (2560, 1024), "v_proj": (2560, 1024),
+    "o_proj": (4096, 2560), "gate_proj": (2560, 9728), "up_proj": (2560, 9728),
+    "down_proj": (9728, 2560),
+}
+QWEN3_4B_LAYERS = 36
+
+
+def _mask_row_padding(packed: torch.Tensor, nbits: int) -> torch.Tensor:
+    """Zero the stream bits at positions >= nbits of every row."""
+    rem = nbits % 8
+    if rem:
+        packed[:, -1] &= (1 << rem) - 1
+    return packed
+
+
+def pack_bits_le(bits01: torch.Tensor) -> torch.Tensor:
+    """Pack a 1-D 0/1 tensor little-endian into uint8 [1, ceil(len/8)]."""
+    n = bits01.numel()
+    pad = (-n) % 8
+    b = torch.nn.functional.pad(bits01.to(torch.int32).reshape(1, -1), (0, pad))
+    w = 1 << torch.arange(8, dtype=torch.int32)
+    return (b.reshape(1, -1, 8) * w).sum(-1).to(torch.uint8)
+
+
+def make_payload(n: int, d: int, bits: int, n_states: int = 64, seed: int = 0,
+                 bias: bool = False, codebook: torch.Tensor | None = None) -> dict:
+    """A seeded format-v2 payload of an n x d packed linear (CPU tensors)."""
+    if bits < 1 or bits > 7:
+        raise ValueError(f"bits must be in [1, 7], got {bits}")
+    block = d & -d
+    if block < 2:
+        raise ValueError(f"in_features={d} has no power-of-2 factor")
+    gen = torch.Generator().manual_seed(seed)
+    path = torch.randint(0, 256, (n, (d + 7) // 8), generator=gen, dtype=torch.uint8)
+    _mask_row_padding(path, d)
+    member = None
+    if bits > 1:
+        mb = d * (bits - 1)
+        member = torch.randint(0, 256, (n, (mb + 7) // 8), generator=gen, dtype=torch.uint8)
+        _mask_row_padding(member, mb)
+    scales = (torch.randn(n, generator=gen).abs() * 0.02 + 1e-3).to(torch.float16)
+    s = torch.exp(torch.randn(d, generator=gen) * 0.25)
+    inv_equil = (1.0 / s.to(torch.float16).float()).to(torch.float16)
+    signs01 = torch.randint(0, 2, (d,), generator=gen, dtype=torch.int64)
+    b = (torch.randn(n, generator=gen) * 0.1).to(torch.float16) if bias else None
+    cb = default_codebook(bits, n_states) if codebook is None else codebook.to(torch.float16)
+    return {
+        "format": 2, "n": n, "d": d, "bits": bits, "n_states": n_states, "block": block,
+        "path_packed": path, "member_packed": member, "scales": scales,
+        "signs_packed": pack_bits_le(signs01), "inv_equil": inv_equil,
+        "codebook": cb, "bias": b, "seed": seed,
+    }
+
+
+def make_activation(batch: int, d: int, seed: int = 0, outlier_frac: float = 0.01,
+                    outlier_scale: float = 20.0) -> torch.Tensor:
+    """fp16 N(0,1) [batch, d] with ceil(outlier_frac*d) channels scaled x20."""
+    gen = torch.Generator().manual_seed(seed)
+    x = torch.randn(batch, d, generator=gen)
+    k = math.ceil(outlier_frac * d)
+    idx = torch.randperm(d, generator=gen)[:k]
+    x[:, idx] *= outlier_scale
+    return x.to(torch.float16)
+
+
+def payload_to(payload: dict, device) -> dict:
+    """Copy of a payload with every tensor moved to ``device``."""
+    return {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in payload.items()}
+
+
+def payload_numpy(payload: dict) -> dict:
+    """Copy of a payload with every tensor as a CPU numpy array."""
+    return {k: (v.detach().cpu().numpy() if isinstance(v, torch.Tensor) else v)
+            for k, v in payload.items()}
