@@ -65,6 +65,12 @@ int tp_subset_lut(int n_states, uint8_t* lut_out, int lut_len);
 int tp_fwht_scale(const uint16_t* x, const uint16_t* rot_scale, uint16_t* z,
                   int64_t batch, int64_t d, int64_t block, void* stream);
 
+/* tp_fwht_scale writing z with row stride ldz >= d and zero-filling columns
+ * [d, ldz) -- the zero-padded activation layout tp_tcq_gemv_tiled reads
+ * (ldz = the z_cols reported by tp_tiled_layout). */
+int tp_fwht_scale_padded(const uint16_t* x, const uint16_t* rot_scale, uint16_t* z,
+                         int64_t batch, int64_t d, int64_t block, int64_t ldz, void* stream);
+
 /* out = blockFWHT(x * pre_scale) * post_scale over `rows` rows of length d
  * (either scale may be NULL), fp32 butterflies, fp16 in/out.  With
  * pre_scale = NULL and post_scale = rot_scale this is the load-time fold of
@@ -115,6 +121,58 @@ int tp_tcq_gemv(const uint16_t* z, int64_t batch,
                 const uint16_t* scales, const uint16_t* codebook, const uint16_t* bias,
                 int64_t n, int64_t d, int bits, int n_states,
                 uint16_t* y, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Bandwidth path: device layout + MFMA decode-GEMV (bits 2 and 3; re-tiling
+ * also accepts bits 4)
+ * ------------------------------------------------------------------------- */
+
+/* Geometry of the device layout of an n x d linear at `bits`: 16-row tiles,
+ * 64-column segments (padded to a multiple of 4).  Reports the tile and
+ * segment counts, the byte sizes of the re-tiled path and member streams
+ * (exactly n_pad * d_pad * bits / 8 together), and the padded activation
+ * width z_cols.  Any output pointer may be NULL.  Host only.
+ * Replaces the load-time stream build of turbopress/runtime.py:253-277
+ * (mode "triton"), which re-packed (k+1)-bit level codes; this layout stays
+ * at the true k bits per weight. */
+int tp_tiled_layout(int64_t n, int64_t d, int bits, int64_t* tiles, int64_t* segments,
+                    int64_t* path_bytes, int64_t* member_bytes, int64_t* z_cols);
+
+/* Re-tile the natural format-v2 path/member streams of an n x d linear into
+ * the device layout (both outputs 16-byte aligned, sizes from
+ * tp_tiled_layout).  Bijective on the weights; padding is zero.
+ * Replaces turbopress/runtime.py:253-277. */
+int tp_retile(const uint8_t* path, int64_t path_stride, const uint8_t* member,
+              int64_t member_stride, int64_t n, int64_t d, int bits,
+              uint8_t* path_tiled, uint8_t* member_tiled, void* stream);
+
+/* Bytes of split-K workspace tp_tcq_gemv_tiled needs for n rows at `batch`
+ * (0 for invalid sizes).  The workspace must be zero before the first call;
+ * every call leaves it zero again, so one allocation serves any number of
+ * calls (and graph replays) on one stream. */
+int64_t tp_gemv_workspace_bytes(int64_t n, int64_t batch);
+
+/* y[b, r] = fp16(scale[r] * sum_c codebook[level[r, c]] * z[b, c]) (+ bias),
+ * reading the device layout.  z: fp16 [batch, ldz] rotated activations, zero
+ * in columns [d, ldz), ldz >= z_cols and a multiple of 8, 16-byte aligned;
+ * y: fp16 [batch, ldy]; batch in [1, 32]; bits in {2, 3}; n_states in
+ * {4, 8, 16, 64}.  Calls that overlap on one workspace race.
+ * Replaces turbopress/triton_kernel.py:132-157 (packed_gemv). */
+int tp_tcq_gemv_tiled(const uint16_t* z, int64_t ldz, int64_t batch,
+                      const uint8_t* path_tiled, const uint8_t* member_tiled,
+                      const uint16_t* scales, const uint16_t* codebook, const uint16_t* bias,
+                      int64_t n, int64_t d, int bits, int n_states,
+                      uint16_t* y, int64_t ldy, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
+/* Decode the device layout through the same decode path the tiled GEMV uses:
+ * w[r, c] = fp16(f32(codebook[level]) * f32(scales[r])), fp16 [n, out_stride].
+ * bits in {2, 3}.  The bit-exact check of the bandwidth path.
+ * Replaces turbopress/runtime.py:291-301 (decode_rows) for this layout. */
+int tp_decode_tiled(const uint8_t* path_tiled, const uint8_t* member_tiled,
+                    const uint16_t* scales, const uint16_t* codebook,
+                    int64_t n, int64_t d, int bits, int n_states,
+                    uint16_t* w_out, int64_t out_stride, void* stream);
 
 #ifdef __cplusplus
 }

@@ -56,7 +56,7 @@ def test_fwht_scale_rejects_bad_block(cuda):
 
 # -------------------------------------------------------------------- decode
 DECODE_CASES = [(n, d, k, s) for s in (4, 8, 16, 64) for (n, d, k) in
-                ((5, 77, 1), (9, 96, 2), (7, 101, 3), (3, 130, 4), (4, 64, 5), (2, 40, 7))]
+                ((5, 78, 1), (9, 96, 2), (7, 102, 3), (3, 130, 4), (4, 64, 5), (2, 40, 7))]
 
 
 @pytest.mark.parametrize("n,d,bits,n_states", DECODE_CASES)

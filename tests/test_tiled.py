@@ -1,0 +1,124 @@
+"""Bandwidth path (device layout + MFMA decode-GEMV) vs the CPU oracle (GPU).
+
+The decode check runs the GEMV kernel's own decode front-end (subset bits by
+funnel-shift XORs, pair-table lookups) through tp_decode_tiled and requires
+bit-exact fp16 weights; GEMV outputs must be within max-rel 2e-3 of the fp64
+product on the same decoded weights.  Shapes cover ragged rows (n not a
+multiple of 16), ragged columns (d not a multiple of 64/256), single-unit and
+split-K tiles, every supported trellis, and batches across the 16-column
+MFMA tiles (1, 3, 16, 17, 32, 40).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tcq_oracle as O
+from turbopress_amd.synthetic import (
+    QWEN3_4B_LAYER, make_activation, make_payload, payload_numpy)
+
+pytestmark = pytest.mark.gpu
+
+GEMV_TOL = 2e-3
+
+DECODE_CASES = [
+    (16, 64, 3, 64), (17, 64, 2, 64), (33, 576, 2, 64), (40, 1000, 3, 64),
+    (5, 200, 3, 16), (31, 328, 2, 8), (20, 130, 3, 4), (48, 2560, 3, 64), (64, 9728, 2, 64),
+]
+
+
+@pytest.mark.parametrize("n,d,bits,n_states", DECODE_CASES)
+def test_tiled_decode_bit_exact(cuda, n, d, bits, n_states):
+    from turbopress_amd.runtime import PackedTCQLinear
+    p = make_payload(n, d, bits, n_states, seed=n + 7 * d)
+    lin = PackedTCQLinear(p, mode="hip")
+    assert lin.tiled_packed is not None and lin.path_packed is None
+    got = lin.decode_rows(0, n).cpu().numpy()
+    ref = O.decode_rows(payload_numpy(p))
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+def test_retiled_bytes_are_true_rate(cuda):
+    from turbopress_amd.hip_kernel import tiled_layout
+    for (d, n) in QWEN3_4B_LAYER.values():
+        for bits in (2, 3, 4):
+            g = tiled_layout(n, d, bits)
+            assert g["path_bytes"] + g["member_bytes"] == g["tiles"] * 16 * g["segments"] * 64 * bits // 8
+            assert g["tiles"] * 16 == -(-n // 16) * 16 and g["z_cols"] >= d
+
+
+GEMV_CASES = [
+    # n, d, bits, S, batch
+    (1536, 576, 2, 64, 1),
+    (192, 256, 3, 64, 2),
+    (100, 700, 3, 16, 3),
+    (4096, 2560, 3, 64, 1),
+    (1024, 2560, 3, 64, 16),
+    (2560, 9728, 3, 64, 17),
+    (9728, 2560, 2, 64, 32),
+    (300, 512, 3, 8, 40),
+    (2560, 4096, 3, 64, 4),
+]
+
+
+@pytest.mark.parametrize("n,d,bits,n_states,batch", GEMV_CASES)
+def test_tiled_gemv_matches_fp64(cuda, n, d, bits, n_states, batch):
+    from turbopress_amd.hip_kernel import packed_gemv
+    from turbopress_amd.runtime import PackedTCQLinear
+    p = make_payload(n, d, bits, n_states, seed=n * 3 + d)
+    lin = PackedTCQLinear(p, mode="hip")
+    z = torch.randn(batch, d, generator=torch.Generator().manual_seed(2)).to(torch.float16)
+    y = packed_gemv(z.to(cuda), lin).float().cpu().numpy()
+    ref = O.gemv_fp64(payload_numpy(p), z.numpy().astype(np.float64))
+    assert O.max_rel(y, ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("name", sorted(QWEN3_4B_LAYER))
+def test_qwen3_4b_forward_matches_tiled_oracle(cuda, name):
+    """Config 2 shapes, one layer, batch 1: rotation + GEMV end to end."""
+    from turbopress_amd.runtime import PackedTCQLinear
+    d, n = QWEN3_4B_LAYER[name]
+    p = make_payload(n, d, 3, 64, seed=len(name) * 31 + n)
+    lin = PackedTCQLinear(p, mode="hip")
+    x = make_activation(1, d, seed=3)
+    y = lin(x.to(cuda)).float().cpu().numpy()
+    assert O.max_rel(y, O.tiled_forward(payload_numpy(p), x.numpy())) <= GEMV_TOL
+
+
+def test_workspace_returns_to_zero_and_calls_repeat(cuda):
+    from turbopress_amd.runtime import PackedTCQLinear
+    p = make_payload(2560, 9728, 3, 64, seed=5, bias=True)
+    lin = PackedTCQLinear(p, mode="hip")
+    x = make_activation(2, 9728, seed=4).to(cuda)
+    ys = [lin(x) for _ in range(3)]
+    torch.cuda.synchronize()
+    assert int(lin._gemv_ws.count_nonzero()) == 0
+    for y in ys[1:]:
+        assert float((y.float() - ys[0].float()).abs().max()) <= 2e-3 * float(ys[0].float().abs().max())
+    ref = O.tiled_forward(payload_numpy(p), x.cpu().numpy())
+    assert O.max_rel(ys[0].float().cpu().numpy(), ref) <= GEMV_TOL
+
+
+def test_graph_replays_match_eager(cuda):
+    from turbopress_amd.runtime import PackedTCQLinear
+    lins, xs = [], []
+    for i, (d, n) in enumerate([(2560, 4096), (4096, 2560), (2560, 9728)]):
+        lins.append(PackedTCQLinear(make_payload(n, d, 3, 64, seed=40 + i), mode="hip"))
+        xs.append(make_activation(1, d, seed=i).to(cuda))
+    eager = [lin(x).clone() for lin, x in zip(lins, xs)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for lin, x in zip(lins, xs):
+            lin(x)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        outs = [lin(x) for lin, x in zip(lins, xs)]
+    for rep in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert float((o.float() - e.float()).abs().max()) <= 2e-3 * float(e.float().abs().max()), rep
+        _ = [lin(x) for lin, x in zip(lins, xs)]  # eager work between replays
+        torch.cuda.synchronize()

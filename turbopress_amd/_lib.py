@@ -37,6 +37,14 @@ SIGNATURES: dict[str, tuple] = {
     "tp_window_decode_levels": (c_int, [_P, _I64, _P, _I64, _I64, _I64, c_int, c_int, _P, _I64, _P]),
     "tp_decode_rows": (c_int, [_P, _I64, _P, _I64, _P, _P, _I64, _I64, c_int, c_int, _P, _I64, _P]),
     "tp_tcq_gemv": (c_int, [_P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I64, c_int, c_int, _P, _P]),
+    "tp_fwht_scale_padded": (c_int, [_P, _P, _P, _I64, _I64, _I64, _I64, _P]),
+    "tp_tiled_layout": (c_int, [_I64, _I64, c_int, POINTER(c_int64), POINTER(c_int64),
+                                POINTER(c_int64), POINTER(c_int64), POINTER(c_int64)]),
+    "tp_retile": (c_int, [_P, _I64, _P, _I64, _I64, _I64, c_int, _P, _P, _P]),
+    "tp_gemv_workspace_bytes": (c_int64, [_I64, _I64]),
+    "tp_tcq_gemv_tiled": (c_int, [_P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _I64, c_int, c_int,
+                                  _P, _I64, _P, _I64, _P]),
+    "tp_decode_tiled": (c_int, [_P, _P, _P, _P, _I64, _I64, c_int, c_int, _P, _I64, _P]),
 }
 
 _LIB: ctypes.CDLL | None = None

@@ -21,14 +21,14 @@ template <int EPT>
 __global__ void __launch_bounds__(256)
 fwht_scale_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ rs,
                   const uint16_t* __restrict__ post, uint16_t* __restrict__ z, int64_t d,
-                  int block, float inv_norm_div) {
+                  int64_t ldz, int block, float inv_norm_div) {
   extern __shared__ float buf[];
   const int64_t row = blockIdx.y;
   const int64_t base = (int64_t)blockIdx.x * block;
   const uint16_t* xr = x + row * d + base;
   const uint16_t* rr = rs ? rs + base : nullptr;
   const uint16_t* pr = post ? post + base : nullptr;
-  uint16_t* zr = z + row * d + base;
+  uint16_t* zr = z + row * ldz + base;
   const int nchunks = block / EPT;  // EPT-element chunks, one per thread per pass
   const int t = threadIdx.x;
 
@@ -70,6 +70,11 @@ fwht_scale_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ r
     if (pr) v *= h2f(pr[i]);
     zr[i] = f2h(v);
   }
+  // The last block of a row also clears the padding columns [d, ldz).
+  if (blockIdx.x == gridDim.x - 1) {
+    uint16_t* zp = z + row * ldz;
+    for (int64_t i = d + t; i < ldz; i += blockDim.x) zp[i] = 0;
+  }
 }
 
 }  // namespace tp
@@ -77,9 +82,9 @@ fwht_scale_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ r
 namespace tp {
 
 int block_fwht(const uint16_t* x, const uint16_t* pre, const uint16_t* post, uint16_t* z,
-               int64_t rows, int64_t d, int64_t block, void* stream) {
+               int64_t rows, int64_t d, int64_t block, int64_t ldz, void* stream) {
   if (!x || !z) return TP_ERR_NULL_POINTER;
-  if (rows < 0 || d <= 0) return TP_ERR_BAD_DIMS;
+  if (rows < 0 || d <= 0 || ldz < d) return TP_ERR_BAD_DIMS;
   if (block < 1 || (block & (block - 1)) || d % block || block > kRotMaxBlock) return TP_ERR_BAD_BLOCK;
   if (rows == 0) return TP_OK;
   if (rows > 65535) return TP_ERR_BAD_DIMS;
@@ -93,10 +98,10 @@ int block_fwht(const uint16_t* x, const uint16_t* pre, const uint16_t* post, uin
   const size_t lds = (size_t)block * sizeof(float);
   hipStream_t s = (hipStream_t)stream;
   switch (ept) {
-    case 8: hipLaunchKernelGGL(fwht_scale_kernel<8>, grid, dim3(threads), lds, s, x, pre, post, z, d, (int)block, div); break;
-    case 4: hipLaunchKernelGGL(fwht_scale_kernel<4>, grid, dim3(threads), lds, s, x, pre, post, z, d, (int)block, div); break;
-    case 2: hipLaunchKernelGGL(fwht_scale_kernel<2>, grid, dim3(threads), lds, s, x, pre, post, z, d, (int)block, div); break;
-    default: hipLaunchKernelGGL(fwht_scale_kernel<1>, grid, dim3(threads), lds, s, x, pre, post, z, d, (int)block, div); break;
+    case 8: hipLaunchKernelGGL(fwht_scale_kernel<8>, grid, dim3(threads), lds, s, x, pre, post, z, d, ldz, (int)block, div); break;
+    case 4: hipLaunchKernelGGL(fwht_scale_kernel<4>, grid, dim3(threads), lds, s, x, pre, post, z, d, ldz, (int)block, div); break;
+    case 2: hipLaunchKernelGGL(fwht_scale_kernel<2>, grid, dim3(threads), lds, s, x, pre, post, z, d, ldz, (int)block, div); break;
+    default: hipLaunchKernelGGL(fwht_scale_kernel<1>, grid, dim3(threads), lds, s, x, pre, post, z, d, ldz, (int)block, div); break;
   }
   return launch_status();
 }
@@ -106,11 +111,18 @@ int block_fwht(const uint16_t* x, const uint16_t* pre, const uint16_t* post, uin
 extern "C" int tp_fwht_scale(const uint16_t* x, const uint16_t* rot_scale, uint16_t* z,
                              int64_t batch, int64_t d, int64_t block, void* stream) {
   if (!rot_scale) return TP_ERR_NULL_POINTER;
-  return tp::block_fwht(x, rot_scale, nullptr, z, batch, d, block, stream);
+  return tp::block_fwht(x, rot_scale, nullptr, z, batch, d, block, d, stream);
+}
+
+extern "C" int tp_fwht_scale_padded(const uint16_t* x, const uint16_t* rot_scale, uint16_t* z,
+                                    int64_t batch, int64_t d, int64_t block, int64_t ldz,
+                                    void* stream) {
+  if (!rot_scale) return TP_ERR_NULL_POINTER;
+  return tp::block_fwht(x, rot_scale, nullptr, z, batch, d, block, ldz, stream);
 }
 
 extern "C" int tp_block_fwht_rows(const uint16_t* x, const uint16_t* pre_scale,
                                   const uint16_t* post_scale, uint16_t* out,
                                   int64_t rows, int64_t d, int64_t block, void* stream) {
-  return tp::block_fwht(x, pre_scale, post_scale, out, rows, d, block, stream);
+  return tp::block_fwht(x, pre_scale, post_scale, out, rows, d, block, d, stream);
 }

@@ -1,0 +1,697 @@
+// Bandwidth path: device ("tiled") layout of the packed streams and the
+// MFMA decode-GEMV that reads it.
+//
+// Device layout (exactly k bits per weight plus zero padding; a bijective
+// re-arrangement of the reference's format-v2 streams, turbopress/runtime.py:73-100):
+//   * rows are grouped in tiles of 16, columns in segments of 64; the number
+//     of segments G is padded to a multiple of 4 (one "unit" = 4 segments);
+//   * path words  [T][G][16 rows][2]:  X0, X1 with
+//        X_x bit 2j   = path bit of column 64g + 16x + j        (first half)
+//        X_x bit 2j+1 = path bit of column 64g + 32 + 16x + j   (second half)
+//   * member words [T][G][16 rows][MW]:
+//        k=3: M[x][h] (x = 0,1; h = first/second half), bits 2j..2j+1 = member
+//             of column 64g + 32h + 16x + j (the reference's own bit order);
+//        k=2: W[x], bits 4p..4p+1 = members of columns 64g + 16x + 2p, +1 and
+//             bits 4p+2..4p+3 = members of columns 64g + 32 + 16x + 2p, +1;
+//        k=4: the k=3 words of the low two member bits, then the k=2 words of
+//             the high member bit (MW = 6).
+//
+// Decode (per lane, 32 weights per path word; reference contract
+// turbopress/runtime.py:122-139): the subset bits are parities of the path
+// window with the trellis generators, i.e. XORs of the path stream delayed by
+// each generator tap.  On the interleaved word a delay of t columns is a left
+// funnel shift by 2t bits across (current word, previous word), so both
+// subset bits of 32 weights cost ~13 ALU ops.  Two weights' (subset, member)
+// bits form one byte that indexes a 256-entry table of fp16 pairs
+// (cb[level_a], cb[level_b]); the table is replicated 64x in LDS so every lane
+// reads its own bank (no conflicts).  The pairs feed
+// v_mfma_f32_16x16x32_f16 (rows x K) against the rotated activations (K x batch).
+// The row scale is applied once at the end (turbopress/triton_kernel.py:70-73,123).
+#include "tp_common.h"
+
+namespace tp {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kTileRows = 16;
+constexpr int kSegCols = 64;
+constexpr int kWavesPerGroup = 8;                 // waves per workgroup
+constexpr int kGroupThreads = 64 * kWavesPerGroup;
+constexpr int kTableWords = 256 * 64;            // 64 KiB
+constexpr int kMaxInlineLinears = 4;
+
+__host__ __device__ constexpr int member_words(int bits) {
+  return bits == 2 ? 2 : bits == 3 ? 4 : bits == 4 ? 6 : 0;
+}
+
+// Delay mask of a window-coordinate generator: bit t set when the subset bit
+// XORs in the path bit t columns back.
+__host__ __device__ constexpr uint32_t delay_mask(uint32_t g, int m) {
+  uint32_t gw = ((g >> m) & 1u) << m;
+  for (int j = 0; j < m; ++j) gw |= ((g >> (m - 1 - j)) & 1u) << j;
+  uint32_t dm = 0;
+  for (int j = 0; j <= m; ++j)
+    if ((gw >> j) & 1u) dm |= 1u << (m - j);
+  return dm;
+}
+
+template <int NS> struct TrellisOf;
+template <> struct TrellisOf<4> { static constexpr int m = 2; static constexpr uint32_t g0 = 05, g1 = 07; };
+template <> struct TrellisOf<8> { static constexpr int m = 3; static constexpr uint32_t g0 = 015, g1 = 017; };
+template <> struct TrellisOf<16> { static constexpr int m = 4; static constexpr uint32_t g0 = 023, g1 = 035; };
+template <> struct TrellisOf<64> { static constexpr int m = 6; static constexpr uint32_t g0 = 0133, g1 = 0171; };
+
+// Subset words of the two 16-weight groups carried by one interleaved path word.
+// SA bit 2j / 2j+1 = subset bit 0 / 1 of first-half weight j; SB likewise for
+// the second half.  `prev` is the interleaved word of the 16 preceding columns
+// of each half.
+template <int NS>
+__device__ __forceinline__ void subset_words(uint32_t cur, uint32_t prev, uint32_t& SA, uint32_t& SB) {
+  constexpr int m = TrellisOf<NS>::m;
+  constexpr uint32_t D0 = delay_mask(TrellisOf<NS>::g0, m);
+  constexpr uint32_t D1 = delay_mask(TrellisOf<NS>::g1, m);
+  uint32_t e0 = (D0 & 1u) ? cur : 0u;
+  uint32_t e1 = (D1 & 1u) ? cur : 0u;
+#pragma unroll
+  for (int t = 1; t <= m; ++t) {
+    const uint32_t a = __builtin_amdgcn_alignbit(cur, prev, 32 - 2 * t);
+    if ((D0 >> t) & 1u) e0 ^= a;
+    if ((D1 >> t) & 1u) e1 ^= a;
+  }
+  SA = (e0 & 0x55555555u) | ((e1 << 1) & 0xAAAAAAAAu);
+  SB = ((e0 >> 1) & 0x55555555u) | (e1 & 0xAAAAAAAAu);
+}
+
+// LDS byte address of the lane's copy of table entry `byte b of idx`.
+__device__ __forceinline__ uint32_t table_addr(uint32_t idx, uint32_t laneoff, int b) {
+  return __builtin_amdgcn_perm(idx, laneoff, 0x0C0C0000u | ((4u + b) << 8));
+}
+
+__device__ __forceinline__ uint32_t lds_word(const uint32_t* table, uint32_t byte_addr) {
+  return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(table) + byte_addr);
+}
+
+// Member words consumed with one interleaved path word (x = 0 or 1).
+template <int KB> struct MemberWords;
+template <> struct MemberWords<2> { uint32_t w; };
+template <> struct MemberWords<3> { uint32_t a, b; };
+
+// Decode 32 weights (16 of each half) of one lane into four MFMA A operands:
+// A[0]/A[1] = first-half columns 0-7 / 8-15, A[2]/A[3] = second half.
+template <int KB, int NS>
+__device__ __forceinline__ void decode_word(uint32_t cur, uint32_t prev, const MemberWords<KB>& M,
+                                            const uint32_t* table, uint32_t laneoff, u32x4_t A[4]) {
+  uint32_t SA, SB;
+  subset_words<NS>(cur, prev, SA, SB);
+  uint32_t iae, iao, ibe, ibo;
+  if constexpr (KB == 3) {
+    iae = (SA & 0x0F0F0F0Fu) | ((M.a << 4) & 0xF0F0F0F0u);
+    iao = ((SA >> 4) & 0x0F0F0F0Fu) | (M.a & 0xF0F0F0F0u);
+    ibe = (SB & 0x0F0F0F0Fu) | ((M.b << 4) & 0xF0F0F0F0u);
+    ibo = ((SB >> 4) & 0x0F0F0F0Fu) | (M.b & 0xF0F0F0F0u);
+  } else {
+    iae = (SA & 0x0F0F0F0Fu) | ((M.w << 4) & 0xF0F0F0F0u);
+    iao = ((SA >> 4) & 0x0F0F0F0Fu) | (M.w & 0xF0F0F0F0u);
+    ibe = (SB & 0x0F0F0F0Fu) | ((M.w << 2) & 0xF0F0F0F0u);
+    ibo = ((SB >> 4) & 0x0F0F0F0Fu) | ((M.w >> 2) & 0xF0F0F0F0u);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    A[0][2 * h] = lds_word(table, table_addr(iae, laneoff, h));
+    A[0][2 * h + 1] = lds_word(table, table_addr(iao, laneoff, h));
+    A[1][2 * h] = lds_word(table, table_addr(iae, laneoff, 2 + h));
+    A[1][2 * h + 1] = lds_word(table, table_addr(iao, laneoff, 2 + h));
+    A[2][2 * h] = lds_word(table, table_addr(ibe, laneoff, h));
+    A[2][2 * h + 1] = lds_word(table, table_addr(ibo, laneoff, h));
+    A[3][2 * h] = lds_word(table, table_addr(ibe, laneoff, 2 + h));
+    A[3][2 * h + 1] = lds_word(table, table_addr(ibo, laneoff, 2 + h));
+  }
+}
+
+// Pair table: entry v = (cb[level_a] | cb[level_b] << 16), with the index byte
+// v = [S0a S1a S0b S1b | member bits], replicated in 64 lane copies.
+template <int KB>
+__device__ __forceinline__ uint32_t pair_entry(const uint16_t* cb, uint32_t v) {
+  const uint32_t sa = v & 3u, sb = (v >> 2) & 3u;
+  uint32_t ma, mb;
+  if constexpr (KB == 3) {
+    ma = (v >> 4) & 3u;
+    mb = (v >> 6) & 3u;
+  } else {
+    ma = (v >> 4) & 1u;
+    mb = (v >> 5) & 1u;
+  }
+  return (uint32_t)cb[ma * 4 + sa] | ((uint32_t)cb[mb * 4 + sb] << 16);
+}
+
+template <int KB>
+__device__ void build_pair_table(uint32_t* table, const uint16_t* cb, int tid, int nthreads) {
+  // Each thread writes 16-byte runs (4 lane copies) of one entry.
+  for (int i = tid; i < kTableWords / 4; i += nthreads) {
+    const uint32_t v = (uint32_t)(i >> 4);  // 16 runs of 4 copies per entry
+    const uint32_t e = pair_entry<KB>(cb, v);
+    u32x4_t run = {e, e, e, e};
+    *reinterpret_cast<u32x4_t*>(table + 4 * i) = run;
+  }
+}
+
+struct MemberLoad2 { uint2 v; };
+struct MemberLoad3 { uint4 v; };
+
+// ---------------------------------------------------------------------------
+// descriptors
+// ---------------------------------------------------------------------------
+struct LinearDesc {
+  const uint32_t* path;    // [T][G][16][2]
+  const uint32_t* member;  // [T][G][16][MW]
+  const uint16_t* z;       // rotated activations, fp16 [batch][ldz], zero past d
+  const uint16_t* scales;  // fp16 [n]
+  const uint16_t* bias;    // fp16 [n] or null
+  uint16_t* y;             // fp16 [batch][ldy]
+  float* ws;               // [T*16][16*NBT] fp32 split-K sums (kept zero between calls)
+  uint32_t* cnt;           // [T] split-K unit counters (kept zero between calls)
+  int32_t n, T, G, G4;
+  int32_t ldz, ldy, kg, blocks;  // kg: units per block; blocks: ceil(T/8)*ceil(G4/kg)
+};
+
+struct GemvArgs {
+  LinearDesc lin[kMaxInlineLinears];
+  int32_t n_lin;
+  int32_t total_blocks;
+  int32_t batch;
+  const uint16_t* codebook;
+};
+
+// ---------------------------------------------------------------------------
+// GEMV kernel: persistent workgroups of 8 waves walk the block list; a block
+// is (8 consecutive row tiles, kg units along K); wave w takes tile w.
+// ---------------------------------------------------------------------------
+template <int KB, int NS, int NBT>
+__global__ void __launch_bounds__(kGroupThreads, 2)
+tcq_gemv_tiled_kernel(const GemvArgs a) {
+  __shared__ uint32_t table[kTableWords];
+  constexpr int MW = member_words(KB);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  build_pair_table<KB>(table, a.codebook, tid, kGroupThreads);
+  __syncthreads();
+
+  const int r = lane & 15;   // A row / B,D column (batch)
+  const int q = lane >> 4;   // K block of A and B, row block of D
+  const uint32_t laneoff = (uint32_t)lane << 2;
+  const int batch = a.batch;
+
+  for (int blk = blockIdx.x; blk < a.total_blocks; blk += gridDim.x) {
+    int li = 0, base = 0;
+#pragma unroll
+    for (int i = 0; i < kMaxInlineLinears - 1; ++i) {
+      if (li + 1 < a.n_lin && blk >= base + a.lin[li].blocks) {
+        base += a.lin[li].blocks;
+        ++li;
+      }
+    }
+    const LinearDesc& L = a.lin[li];
+    const int rel = blk - base;
+    const int nkb = (L.G4 + L.kg - 1) / L.kg;
+    const int tb = rel / nkb, kb = rel - tb * nkb;
+    const int t = tb * kWavesPerGroup + wave;
+    if (t >= L.T) continue;
+    const int gu0 = kb * L.kg;
+    const int ngu = min(L.kg, L.G4 - gu0);
+
+    const uint32_t* pt = L.path + (size_t)t * L.G * (kTileRows * 2);
+    const uint32_t* mt = L.member + (size_t)t * L.G * (kTileRows * MW);
+
+    float4_t acc[NBT];
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // Path word X1 of the segment before this block (the lanes of the last
+    // K block hand it to the first K block of the next unit).
+    uint32_t x1_last = 0;
+    if (gu0 > 0) x1_last = pt[((4 * gu0 - 1) * kTileRows + r) * 2 + 1];
+
+    int g = 4 * gu0 + q;
+    uint2 X = *reinterpret_cast<const uint2*>(pt + (g * kTileRows + r) * 2);
+    uint32_t Mw[MW];
+#pragma unroll
+    for (int i = 0; i < MW; ++i) Mw[i] = mt[(g * kTileRows + r) * MW + i];
+
+    for (int u = 0; u < ngu; ++u) {
+      const int gu = gu0 + u;
+      g = 4 * gu + q;
+      uint2 Xn = X;
+      uint32_t Mn[MW];
+#pragma unroll
+      for (int i = 0; i < MW; ++i) Mn[i] = Mw[i];
+      if (u + 1 < ngu) {
+        const int gn = g + 4;
+        Xn = *reinterpret_cast<const uint2*>(pt + (gn * kTileRows + r) * 2);
+#pragma unroll
+        for (int i = 0; i < MW; ++i) Mn[i] = mt[(gn * kTileRows + r) * MW + i];
+      }
+      // B operand: 8 halves of z per MFMA for batch column r (zero past batch).
+      half8_t zb[NBT][8];
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        const int nb = bt * 16 + r;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const int off = (c & 4 ? 16 : 0) + (c & 2 ? 32 : 0) + (c & 1 ? 8 : 0);
+          if (nb < batch)
+            zb[bt][c] = *reinterpret_cast<const half8_t*>(L.z + (size_t)nb * L.ldz + g * kSegCols + off);
+          else
+            zb[bt][c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
+      }
+      // Halo: X1 of segment g-1, from the lane 16 below (K block q-1), or for
+      // q == 0 from the last K block's previous unit; zero at a row start.
+      const uint32_t provide = (q == 3) ? (gu == 0 ? 0u : x1_last) : X.y;
+      const uint32_t halo = (uint32_t)__shfl((int)provide, (lane + 48) & 63, 64);
+      const uint32_t P = ((halo >> 1) & 0x55555555u) | ((X.y << 1) & 0xAAAAAAAAu);
+
+      u32x4_t A[4];
+      MemberWords<KB> m0, m1;
+      if constexpr (KB == 3) {
+        m0.a = Mw[0]; m0.b = Mw[1]; m1.a = Mw[2]; m1.b = Mw[3];
+      } else {
+        m0.w = Mw[0]; m1.w = Mw[1];
+      }
+      decode_word<KB, NS>(X.x, P, m0, table, laneoff, A);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const half8_t av = __builtin_bit_cast(half8_t, A[j]);
+        // chunk index c = (x << 2) | (j >> 1) << 1 | (j & 1) with x = 0
+        const int c = ((j >> 1) << 1) | (j & 1);
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt)
+          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, zb[bt][c], acc[bt], 0, 0, 0);
+      }
+      decode_word<KB, NS>(X.y, X.x, m1, table, laneoff, A);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const half8_t av = __builtin_bit_cast(half8_t, A[j]);
+        const int c = 4 | ((j >> 1) << 1) | (j & 1);
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt)
+          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, zb[bt][c], acc[bt], 0, 0, 0);
+      }
+      x1_last = X.y;
+      X = Xn;
+#pragma unroll
+      for (int i = 0; i < MW; ++i) Mw[i] = Mn[i];
+    }
+
+    // Epilogue.  Lane holds D[4q + i][r]: rows 4q..4q+3 of the tile for batch column r.
+    const int ldws = 16 * NBT;
+    if (ngu == L.G4) {
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        const int nb = bt * 16 + r;
+        if (nb >= batch) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = t * kTileRows + 4 * q + i;
+          if (row >= L.n) continue;
+          uint16_t out = f2h(acc[bt][i] * h2f(L.scales[row]));
+          if (L.bias) out = f2h(h2f(out) + h2f(L.bias[row]));
+          L.y[(size_t)nb * L.ldy + row] = out;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        const int nb = bt * 16 + r;
+        if (nb >= batch) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          atomicAdd(L.ws + (size_t)(t * kTileRows + 4 * q + i) * ldws + bt * 16 + r, acc[bt][i]);
+      }
+      __threadfence();
+      uint32_t old = 0;
+      if (lane == 0) old = atomicAdd(L.cnt + t, (uint32_t)ngu);
+      old = (uint32_t)__shfl((int)old, 0, 64);
+      if (old + (uint32_t)ngu == (uint32_t)L.G4) {
+        __threadfence();
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+          const int nb = bt * 16 + r;
+          if (nb >= batch) continue;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int row = t * kTileRows + 4 * q + i;
+            const float v = atomicExch(L.ws + (size_t)row * ldws + bt * 16 + r, 0.f);
+            if (row >= L.n) continue;
+            uint16_t out = f2h(v * h2f(L.scales[row]));
+            if (L.bias) out = f2h(h2f(out) + h2f(L.bias[row]));
+            L.y[(size_t)nb * L.ldy + row] = out;
+          }
+        }
+        if (lane == 0) atomicExch(L.cnt + t, 0u);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Debug decode of the tiled layout through the GEMV's own decode path:
+// w[row, col] = fp16(f32(pair value) * f32(scale[row])).  One wave per unit.
+// ---------------------------------------------------------------------------
+template <int KB, int NS>
+__global__ void __launch_bounds__(256)
+tiled_decode_kernel(const uint32_t* __restrict__ path, const uint32_t* __restrict__ member,
+                    const uint16_t* __restrict__ scales, const uint16_t* __restrict__ cb,
+                    int n, int d, int T, int G, int G4, uint16_t* __restrict__ w, int64_t ldw) {
+  __shared__ uint32_t table[kTableWords];
+  constexpr int MW = member_words(KB);
+  build_pair_table<KB>(table, cb, threadIdx.x, blockDim.x);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15, q = lane >> 4;
+  const uint32_t laneoff = (uint32_t)lane << 2;
+  const int64_t unit = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (unit >= (int64_t)T * G4) return;
+  const int t = (int)(unit / G4), gu = (int)(unit % G4);
+  const int g = 4 * gu + q;
+  const uint32_t* pt = path + (size_t)t * G * (kTileRows * 2);
+  const uint32_t* mt = member + (size_t)t * G * (kTileRows * MW);
+  const uint2 X = *reinterpret_cast<const uint2*>(pt + (g * kTileRows + r) * 2);
+  const uint32_t halo = g > 0 ? pt[((g - 1) * kTileRows + r) * 2 + 1] : 0u;
+  const uint32_t P = ((halo >> 1) & 0x55555555u) | ((X.y << 1) & 0xAAAAAAAAu);
+  uint32_t Mw[MW];
+  for (int i = 0; i < MW; ++i) Mw[i] = mt[(g * kTileRows + r) * MW + i];
+  MemberWords<KB> mm[2];
+  if constexpr (KB == 3) {
+    mm[0].a = Mw[0]; mm[0].b = Mw[1]; mm[1].a = Mw[2]; mm[1].b = Mw[3];
+  } else {
+    mm[0].w = Mw[0]; mm[1].w = Mw[1];
+  }
+  const int row = t * kTileRows + r;
+  const float sc = row < n ? h2f(scales[row]) : 0.f;
+  for (int x = 0; x < 2; ++x) {
+    u32x4_t A[4];
+    decode_word<KB, NS>(x ? X.y : X.x, x ? X.x : P, mm[x], table, laneoff, A);
+    if (row >= n) continue;
+    for (int j = 0; j < 4; ++j) {
+      for (int v = 0; v < 4; ++v) {
+        for (int e = 0; e < 2; ++e) {
+          const int col = g * kSegCols + (j >> 1) * 32 + 16 * x + 8 * (j & 1) + 2 * v + e;
+          if (col >= d) continue;
+          const uint16_t h = (uint16_t)(A[j][v] >> (16 * e));
+          w[(int64_t)row * ldw + col] = f2h(h2f(h) * sc);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Re-tiling: natural format v2 streams -> device layout.  One thread per
+// (tile, segment, row).  Columns past d and rows past n are zero.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t interleave16(uint32_t a, uint32_t b) {
+  uint32_t o = 0;
+  for (int j = 0; j < 16; ++j) o |= (((a >> j) & 1u) << (2 * j)) | (((b >> j) & 1u) << (2 * j + 1));
+  return o;
+}
+
+__device__ __forceinline__ uint32_t pair_interleave16(uint32_t a, uint32_t b) {
+  uint32_t o = 0;
+  for (int p = 0; p < 8; ++p) o |= (((a >> (2 * p)) & 3u) << (4 * p)) | (((b >> (2 * p)) & 3u) << (4 * p + 2));
+  return o;
+}
+
+__global__ void retile_kernel(const uint8_t* __restrict__ path, int64_t ps,
+                              const uint8_t* __restrict__ member, int64_t ms,
+                              int64_t n, int64_t d, int bits, int64_t T, int64_t G,
+                              uint32_t* __restrict__ out_path, uint32_t* __restrict__ out_member) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= T * G * kTileRows) return;
+  const int r = (int)(idx & 15);
+  const int64_t tg = idx >> 4;
+  const int64_t g = tg % G, t = tg / G;
+  const int64_t row = t * kTileRows + r;
+  uint32_t h[2] = {0, 0};     // path bits of the two halves
+  uint32_t mlo[4] = {0, 0, 0, 0};  // 2-bit member fields per 16-column group
+  uint32_t m1[4] = {0, 0, 0, 0};   // 1-bit member fields per 16-column group
+  if (row < n) {
+    const uint8_t* prow = path + row * ps;
+    const uint8_t* mrow = member ? member + row * ms : nullptr;
+    for (int c = 0; c < kSegCols; ++c) {
+      const int64_t col = g * kSegCols + c;
+      if (col >= d) break;
+      h[c >> 5] |= read_bits_le(prow, ps, col, 1) << (c & 31);
+      if (bits > 1) {
+        const uint32_t mv = read_bits_le(mrow, ms, col * (bits - 1), bits - 1);
+        const int grp = c >> 4, j = c & 15;
+        if (bits == 2) {
+          m1[grp] |= (mv & 1u) << j;
+        } else {
+          mlo[grp] |= (mv & 3u) << (2 * j);
+          if (bits == 4) m1[grp] |= ((mv >> 2) & 1u) << j;
+        }
+      }
+    }
+  }
+  out_path[idx * 2] = interleave16(h[0] & 0xFFFFu, h[1] & 0xFFFFu);
+  out_path[idx * 2 + 1] = interleave16(h[0] >> 16, h[1] >> 16);
+  const int mw = member_words(bits);
+  uint32_t* mo = out_member + idx * mw;
+  // column groups: 0 = first half x=0, 1 = first half x=1, 2 = second half x=0, 3 = second half x=1
+  if (bits == 3 || bits == 4) {
+    mo[0] = mlo[0]; mo[1] = mlo[2]; mo[2] = mlo[1]; mo[3] = mlo[3];
+  }
+  if (bits == 2) {
+    mo[0] = pair_interleave16(m1[0], m1[2]);
+    mo[1] = pair_interleave16(m1[1], m1[3]);
+  } else if (bits == 4) {
+    mo[4] = pair_interleave16(m1[0], m1[2]);
+    mo[5] = pair_interleave16(m1[1], m1[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+struct Geom {
+  int64_t T, G, G4, path_words, member_words;
+};
+
+inline int tiled_geom(int64_t n, int64_t d, int bits, Geom* g) {
+  if (n <= 0 || d <= 0) return TP_ERR_BAD_DIMS;
+  if (bits < 2 || bits > 4) return TP_ERR_UNSUPPORTED_BITS;
+  g->T = (n + kTileRows - 1) / kTileRows;
+  g->G4 = (d + 4 * kSegCols - 1) / (4 * kSegCols);
+  g->G = 4 * g->G4;
+  g->path_words = g->T * g->G * kTileRows * 2;
+  g->member_words = g->T * g->G * kTileRows * member_words(bits);
+  if (g->T > (1 << 26) || g->G > (1 << 20)) return TP_ERR_BAD_DIMS;
+  return TP_OK;
+}
+
+inline int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+}  // namespace tp
+
+using namespace tp;
+
+extern "C" int tp_tiled_layout(int64_t n, int64_t d, int bits, int64_t* tiles, int64_t* segments,
+                               int64_t* path_bytes, int64_t* member_bytes, int64_t* z_cols) {
+  Geom g;
+  int st = tiled_geom(n, d, bits, &g);
+  if (st) return st;
+  if (tiles) *tiles = g.T;
+  if (segments) *segments = g.G;
+  if (path_bytes) *path_bytes = g.path_words * 4;
+  if (member_bytes) *member_bytes = g.member_words * 4;
+  if (z_cols) *z_cols = g.G * kSegCols;
+  return TP_OK;
+}
+
+extern "C" int tp_retile(const uint8_t* path, int64_t path_stride, const uint8_t* member,
+                         int64_t member_stride, int64_t n, int64_t d, int bits,
+                         uint8_t* path_tiled, uint8_t* member_tiled, void* stream) {
+  Geom g;
+  int st = tiled_geom(n, d, bits, &g);
+  if (st) return st;
+  if (!path || !member || !path_tiled || !member_tiled) return TP_ERR_NULL_POINTER;
+  if (path_stride < (d + 7) / 8 || member_stride < (d * (bits - 1) + 7) / 8) return TP_ERR_BAD_DIMS;
+  if (((uintptr_t)path_tiled | (uintptr_t)member_tiled) & 15) return TP_ERR_MISALIGNED;
+  const int64_t threads = g.T * g.G * kTileRows;
+  hipLaunchKernelGGL(retile_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, path, path_stride, member, member_stride, n, d, bits,
+                     g.T, g.G, reinterpret_cast<uint32_t*>(path_tiled),
+                     reinterpret_cast<uint32_t*>(member_tiled));
+  return launch_status();
+}
+
+extern "C" int64_t tp_gemv_workspace_bytes(int64_t n, int64_t batch) {
+  if (n <= 0 || batch <= 0) return 0;
+  const int64_t T = (n + kTileRows - 1) / kTileRows;
+  const int64_t nbt = batch <= 16 ? 1 : 2;
+  return T * kTileRows * 16 * nbt * 4 + T * 4;
+}
+
+extern "C" int tp_decode_tiled(const uint8_t* path_tiled, const uint8_t* member_tiled,
+                               const uint16_t* scales, const uint16_t* codebook,
+                               int64_t n, int64_t d, int bits, int n_states,
+                               uint16_t* w_out, int64_t out_stride, void* stream) {
+  Geom g;
+  int st = tiled_geom(n, d, bits, &g);
+  if (st) return st;
+  if (bits == 4) return TP_ERR_UNSUPPORTED_BITS;
+  if (!path_tiled || !member_tiled || !scales || !codebook || !w_out) return TP_ERR_NULL_POINTER;
+  if (out_stride < d) return TP_ERR_BAD_DIMS;
+  const int64_t units = g.T * g.G4;
+  dim3 grid((unsigned)((units + 3) / 4)), block(256);
+  hipStream_t s = (hipStream_t)stream;
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(path_tiled);
+  const uint32_t* m = reinterpret_cast<const uint32_t*>(member_tiled);
+#define TP_DEC(KB, NS)                                                                            \
+  hipLaunchKernelGGL((tiled_decode_kernel<KB, NS>), grid, block, 0, s, p, m, scales, codebook,  \
+                     (int)n, (int)d, (int)g.T, (int)g.G, (int)g.G4, w_out, out_stride)
+  switch (bits * 100 + n_states) {
+    case 204: TP_DEC(2, 4); break;
+    case 208: TP_DEC(2, 8); break;
+    case 216: TP_DEC(2, 16); break;
+    case 264: TP_DEC(2, 64); break;
+    case 304: TP_DEC(3, 4); break;
+    case 308: TP_DEC(3, 8); break;
+    case 316: TP_DEC(3, 16); break;
+    case 364: TP_DEC(3, 64); break;
+    default: return TP_ERR_UNSUPPORTED_STATES;
+  }
+#undef TP_DEC
+  return launch_status();
+}
+
+namespace tp {
+
+struct TiledLinearArgs {
+  const uint8_t* path_tiled;
+  const uint8_t* member_tiled;
+  const uint16_t* z;
+  int64_t ldz;
+  const uint16_t* scales;
+  const uint16_t* bias;
+  uint16_t* y;
+  int64_t ldy;
+  int64_t n, d;
+  void* workspace;
+  int64_t workspace_bytes;
+};
+
+template <int KB, int NS, int NBT>
+void launch_gemv(const GemvArgs& a, int grid, hipStream_t s) {
+  hipLaunchKernelGGL((tcq_gemv_tiled_kernel<KB, NS, NBT>), dim3(grid), dim3(kGroupThreads), 0, s, a);
+}
+
+int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
+                     int bits, int n_states, void* stream) {
+  if (n_lin < 1 || n_lin > kMaxInlineLinears) return TP_ERR_BAD_DIMS;
+  if (!codebook) return TP_ERR_NULL_POINTER;
+  if (bits != 2 && bits != 3) return TP_ERR_UNSUPPORTED_BITS;
+  if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
+  const int nbt = batch <= 16 ? 1 : 2;
+  GemvArgs a;
+  a.n_lin = n_lin;
+  a.batch = (int)batch;
+  a.codebook = codebook;
+  int64_t units_total = 0;
+  for (int i = 0; i < n_lin; ++i) {
+    Geom g;
+    int st = tiled_geom(ls[i].n, ls[i].d, bits, &g);
+    if (st) return st;
+    units_total += g.T * g.G4;
+  }
+  const int cus = device_cu_count();
+  const int64_t max_waves = (int64_t)cus * 2 * kWavesPerGroup;
+  // Units per block along K: spread the units over about one wave slot each.
+  int64_t total_blocks = 0;
+  for (int i = 0; i < n_lin; ++i) {
+    const TiledLinearArgs& l = ls[i];
+    if (!l.path_tiled || !l.member_tiled || !l.z || !l.scales || !l.y) return TP_ERR_NULL_POINTER;
+    Geom g;
+    tiled_geom(l.n, l.d, bits, &g);
+    if (l.ldz < g.G * kSegCols || (l.ldz & 7) || l.ldy < l.n) return TP_ERR_BAD_DIMS;
+    if (((uintptr_t)l.z & 15) || ((uintptr_t)l.path_tiled & 15) || ((uintptr_t)l.member_tiled & 15))
+      return TP_ERR_MISALIGNED;
+    int64_t kg = (units_total + max_waves - 1) / max_waves;
+    if (kg < 1) kg = 1;
+    if (kg > g.G4) kg = g.G4;
+    const int64_t nkb = (g.G4 + kg - 1) / kg;
+    const int64_t blocks = ((g.T + kWavesPerGroup - 1) / kWavesPerGroup) * nkb;
+    LinearDesc& L = a.lin[i];
+    L.path = reinterpret_cast<const uint32_t*>(l.path_tiled);
+    L.member = reinterpret_cast<const uint32_t*>(l.member_tiled);
+    L.z = l.z;
+    L.scales = l.scales;
+    L.bias = l.bias;
+    L.y = l.y;
+    L.n = (int32_t)l.n;
+    L.T = (int32_t)g.T;
+    L.G = (int32_t)g.G;
+    L.G4 = (int32_t)g.G4;
+    L.ldz = (int32_t)l.ldz;
+    L.ldy = (int32_t)l.ldy;
+    L.kg = (int32_t)kg;
+    L.blocks = (int32_t)blocks;
+    if (nkb > 1) {
+      const int64_t need = g.T * kTileRows * 16 * nbt * 4 + g.T * 4;
+      if (!l.workspace || l.workspace_bytes < need) return TP_ERR_WORKSPACE;
+      if ((uintptr_t)l.workspace & 15) return TP_ERR_MISALIGNED;
+      L.ws = reinterpret_cast<float*>(l.workspace);
+      L.cnt = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(l.workspace) + g.T * kTileRows * 16 * nbt * 4);
+    } else {
+      L.ws = nullptr;
+      L.cnt = nullptr;
+    }
+    total_blocks += blocks;
+  }
+  for (int i = n_lin; i < kMaxInlineLinears; ++i) a.lin[i] = a.lin[0];
+  if (total_blocks > INT32_MAX) return TP_ERR_BAD_DIMS;
+  a.total_blocks = (int32_t)total_blocks;
+  int grid = (int)(total_blocks < (int64_t)cus * 2 ? total_blocks : (int64_t)cus * 2);
+  hipStream_t s = (hipStream_t)stream;
+#define TP_GEMV(KB, NS)                                             \
+  (nbt == 1 ? launch_gemv<KB, NS, 1>(a, grid, s) : launch_gemv<KB, NS, 2>(a, grid, s))
+  switch (bits * 100 + n_states) {
+    case 204: TP_GEMV(2, 4); break;
+    case 208: TP_GEMV(2, 8); break;
+    case 216: TP_GEMV(2, 16); break;
+    case 264: TP_GEMV(2, 64); break;
+    case 304: TP_GEMV(3, 4); break;
+    case 308: TP_GEMV(3, 8); break;
+    case 316: TP_GEMV(3, 16); break;
+    case 364: TP_GEMV(3, 64); break;
+    default: return TP_ERR_UNSUPPORTED_STATES;
+  }
+#undef TP_GEMV
+  return launch_status();
+}
+
+}  // namespace tp
+
+extern "C" int tp_tcq_gemv_tiled(const uint16_t* z, int64_t ldz, int64_t batch,
+                                 const uint8_t* path_tiled, const uint8_t* member_tiled,
+                                 const uint16_t* scales, const uint16_t* codebook, const uint16_t* bias,
+                                 int64_t n, int64_t d, int bits, int n_states,
+                                 uint16_t* y, int64_t ldy, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
+  TiledLinearArgs l{path_tiled, member_tiled, z, ldz, scales, bias, y, ldy, n, d, workspace, workspace_bytes};
+  return gemv_tiled_group(&l, 1, batch, codebook, bits, n_states, stream);
+}

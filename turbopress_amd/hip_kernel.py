@@ -16,7 +16,10 @@ from torch import Tensor
 from turbopress_amd import _lib
 
 __all__ = ["HAS_HIP", "fwht_scale", "packed_gemv", "decode_rows", "window_decode_levels",
-           "subset_lut", "current_stream_ptr"]
+           "subset_lut", "current_stream_ptr", "tiled_layout", "retile", "TILED_BITS"]
+
+# bits per weight served by the device-layout MFMA kernels
+TILED_BITS = (2, 3)
 
 
 def _has_hip() -> bool:
@@ -113,11 +116,16 @@ def packed_gemv(z: Tensor, layer, bias: Tensor | None = None) -> Tensor:
     ``n_states``, ``scales``, ``codebook`` and the packed streams
     ``path_packed``/``member_packed``.  Returns fp16 [..., n]."""
     _require_cuda(z, "z")
-    if getattr(layer, "path_packed", None) is None:
-        raise RuntimeError("layer was not built with mode='hip'")
     n, d = layer.out_features, layer.in_features
     flat = z.reshape(-1, d).to(torch.float16).contiguous()
     out = torch.empty(flat.shape[0], n, dtype=torch.float16, device=z.device)
+    if getattr(layer, "tiled_packed", None) is not None:
+        ldz = layer._tiled_geo["z_cols"]
+        zpad = flat if ldz == d else torch.nn.functional.pad(flat, (0, ldz - d))
+        gemv_tiled(zpad, layer, bias, out)
+        return out.reshape(*z.shape[:-1], n)
+    if getattr(layer, "path_packed", None) is None:
+        raise RuntimeError("layer was not built with mode='hip'")
     path, mem = layer.path_packed, layer.member_packed
     st = _lib.lib().tp_tcq_gemv(
         flat.data_ptr(), flat.shape[0], path.data_ptr(), path.stride(0),
@@ -127,3 +135,81 @@ def packed_gemv(z: Tensor, layer, bias: Tensor | None = None) -> Tensor:
         n, d, layer.bits, layer.n_states, out.data_ptr(), current_stream_ptr(z.device))
     _lib.check(st, "packed_gemv")
     return out.reshape(*z.shape[:-1], n)
+
+
+# ---------------------------------------------------------------------------
+# bandwidth path: device layout + MFMA decode-GEMV
+# ---------------------------------------------------------------------------
+def tiled_layout(n: int, d: int, bits: int) -> dict:
+    """Geometry of the device layout (tp_tiled_layout)."""
+    import ctypes
+    vals = [ctypes.c_int64() for _ in range(5)]
+    _lib.check(_lib.lib().tp_tiled_layout(n, d, bits, *[ctypes.byref(v) for v in vals]), "tiled_layout")
+    keys = ("tiles", "segments", "path_bytes", "member_bytes", "z_cols")
+    return dict(zip(keys, (v.value for v in vals)))
+
+
+def retile(path_packed: Tensor, member_packed: Tensor, n: int, d: int, bits: int) -> Tensor:
+    """One uint8 device buffer [path words | member words] in the kernel's
+    layout (replaces the load-time stream build of runtime.py:253-277)."""
+    _require_cuda(path_packed, "path_packed")
+    geo = tiled_layout(n, d, bits)
+    pb, mb = geo["path_bytes"], geo["member_bytes"]
+    buf = torch.empty(pb + mb, dtype=torch.uint8, device=path_packed.device)
+    path, mem = path_packed.contiguous(), member_packed.contiguous()
+    st = _lib.lib().tp_retile(path.data_ptr(), path.stride(0), mem.data_ptr(), mem.stride(0),
+                              n, d, bits, buf.data_ptr(), buf.data_ptr() + pb,
+                              current_stream_ptr(path.device))
+    _lib.check(st, "retile")
+    return buf
+
+
+def gemv_workspace(n: int, batch: int, device) -> Tensor:
+    nbytes = int(_lib.lib().tp_gemv_workspace_bytes(n, batch))
+    return torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def decode_tiled(layer) -> Tensor:
+    """fp16 rotated weights [n, d] decoded through the tiled GEMV's decode path."""
+    n, d = layer.out_features, layer.in_features
+    buf = layer.tiled_packed
+    out = torch.empty(n, d, dtype=torch.float16, device=buf.device)
+    st = _lib.lib().tp_decode_tiled(buf.data_ptr(), buf.data_ptr() + layer._tiled_geo["path_bytes"],
+                                    layer.scales.data_ptr(), layer.codebook.data_ptr(), n, d,
+                                    layer.bits, layer.n_states, out.data_ptr(), d,
+                                    current_stream_ptr(buf.device))
+    _lib.check(st, "decode_tiled")
+    return out
+
+
+def rotate_padded(x: Tensor, rot_scale: Tensor, block: int, ldz: int) -> Tensor:
+    """fp16 z [B, ldz] = blockFWHT(x * rot_scale) with zero columns [d, ldz)."""
+    _require_cuda(x, "x")
+    d = x.shape[-1]
+    flat = x.reshape(-1, d).to(torch.float16).contiguous()
+    z = torch.empty(flat.shape[0], ldz, dtype=torch.float16, device=x.device)
+    st = _lib.lib().tp_fwht_scale_padded(flat.data_ptr(), rot_scale.data_ptr(), z.data_ptr(),
+                                         flat.shape[0], d, int(block), ldz,
+                                         current_stream_ptr(x.device))
+    _lib.check(st, "fwht_scale_padded")
+    return z
+
+
+def gemv_tiled(zpad: Tensor, layer, bias: Tensor | None, out: Tensor) -> Tensor:
+    """out[B, n] = packed GEMV over the device layout; zpad fp16 [B, ldz]."""
+    n, d = layer.out_features, layer.in_features
+    buf = layer.tiled_packed
+    ws = layer._gemv_ws
+    pb = layer._tiled_geo["path_bytes"]
+    ldz = zpad.shape[1]
+    stream = current_stream_ptr(zpad.device)
+    lib = _lib.lib()
+    for b0 in range(0, zpad.shape[0], 32):
+        nb = min(32, zpad.shape[0] - b0)
+        st = lib.tp_tcq_gemv_tiled(
+            zpad.data_ptr() + 2 * b0 * ldz, ldz, nb, buf.data_ptr(), buf.data_ptr() + pb,
+            layer.scales.data_ptr(), layer.codebook.data_ptr(),
+            0 if bias is None else bias.data_ptr(), n, d, layer.bits, layer.n_states,
+            out.data_ptr() + 2 * b0 * n, n, ws.data_ptr(), ws.numel(), stream)
+        _lib.check(st, "tcq_gemv_tiled")
+    return out

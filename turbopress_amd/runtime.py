@@ -119,10 +119,24 @@ class PackedTCQLinear(nn.Module):
         self.register_buffer("_w_cache", None)
         self.register_buffer("levels_packed", None)
 
+        self.register_buffer("tiled_packed", None)
+        self.register_buffer("_gemv_ws", None, persistent=False)
+        self._tiled_geo = None
         if self.mode == "hip":
-            # The fused kernel reads the true-rate streams directly; expose them
-            # under the attribute scripts check for a device decode stream.
-            self.levels_packed = self.path_packed
+            if self.bits in hk.TILED_BITS:
+                # Load-time re-tile into the MFMA kernel's layout, still at the
+                # true k bits/weight (the reference re-packs (k+1)-bit levels
+                # here, runtime.py:253-277); the natural streams are freed.
+                self._tiled_geo = hk.tiled_layout(self.out_features, d, self.bits)
+                self.tiled_packed = hk.retile(self.path_packed, self.member_packed,
+                                              self.out_features, d, self.bits)
+                self._gemv_ws = hk.gemv_workspace(self.out_features, 32, dev)
+                for name in ("path_packed", "member_packed"):
+                    setattr(self, name, None)
+                self.levels_packed = self.tiled_packed
+            else:
+                # Other rates run the general kernels on the natural streams.
+                self.levels_packed = self.path_packed
         elif self.mode == "cached":
             w_rot = self.decode_rows(0, self.out_features)
             w = torch.empty_like(w_rot)
@@ -153,6 +167,8 @@ class PackedTCQLinear(nn.Module):
     # -- decode -----------------------------------------------------------
     def decode_rows(self, r0: int, r1: int) -> Tensor:
         """Decode rows [r0, r1) of the rotated weight matrix to fp16 (GPU)."""
+        if self.tiled_packed is not None:
+            return hk.decode_tiled(self)[max(0, r0):min(self.out_features, r1)].contiguous()
         return hk.decode_rows(self, r0, r1)
 
     # -- forward ----------------------------------------------------------
@@ -166,6 +182,11 @@ class PackedTCQLinear(nn.Module):
             if self.bias is not None:
                 y = y + self.bias
             return y.to(x.dtype)
+        if self.tiled_packed is not None:
+            zpad = hk.rotate_padded(x, self.rot_scale, self.block, self._tiled_geo["z_cols"])
+            y = torch.empty(zpad.shape[0], self.out_features, dtype=torch.float16, device=x.device)
+            hk.gemv_tiled(zpad, self, self.bias, y)
+            return y.reshape(*x.shape[:-1], self.out_features).to(x.dtype)
         z = hk.fwht_scale(x, self.rot_scale, self.block)
         if self.mode == "hip":
             y = hk.packed_gemv(z, self, bias=self.bias)
@@ -185,6 +206,9 @@ class PackedTCQLinear(nn.Module):
         """Resident weight bytes under the current mode (runtime.py:337-356)."""
         if self._w_cache is not None:
             total = self._w_cache.numel() * self._w_cache.element_size()
+        elif self.tiled_packed is not None:
+            total = self.tiled_packed.numel() + self.signs_packed.numel()
+            total += 2 * (self.inv_equil.numel() + self.rot_scale.numel())
         else:
             total = self.path_packed.numel() + self.signs_packed.numel()
             if self.member_packed is not None:
