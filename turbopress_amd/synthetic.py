@@ -26,7 +26,7 @@ import math
 
 import torch
 
-from turbopress_amd.codebooks import default_codebook
+from turbopress_amd.codebooks import available_codebooks, default_codebook
 
 # Qwen3 decoder-layer projection shapes (in_features -> out_features).
 QWEN3_0_6B_LAYER = {
@@ -59,6 +59,16 @@ def pack_bits_le(bits01: torch.Tensor) -> torch.Tensor:
     return (b.reshape(1, -1, 8) * w).sum(-1).to(torch.uint8)
 
 
+def _synthetic_codebook(bits: int, seed: int) -> torch.Tensor:
+    """Seeded fp16 doubled codebook for rates without a stored default: N(0,1)
+    draws, each Ungerboeck subset cb[j::4] sorted (trellis.py:249-250)."""
+    gen = torch.Generator().manual_seed(10_000 + seed)
+    cb = torch.randn(1 << (bits + 1), generator=gen)
+    for j in range(4):
+        cb[j::4] = cb[j::4].sort().values
+    return cb.to(torch.float16)
+
+
 def make_payload(n: int, d: int, bits: int, n_states: int = 64, seed: int = 0,
                  bias: bool = False, codebook: torch.Tensor | None = None) -> dict:
     """A seeded format-v2 payload of an n x d packed linear (CPU tensors)."""
@@ -80,7 +90,12 @@ def make_payload(n: int, d: int, bits: int, n_states: int = 64, seed: int = 0,
     inv_equil = (1.0 / s.to(torch.float16).float()).to(torch.float16)
     signs01 = torch.randint(0, 2, (d,), generator=gen, dtype=torch.int64)
     b = (torch.randn(n, generator=gen) * 0.1).to(torch.float16) if bias else None
-    cb = default_codebook(bits, n_states) if codebook is None else codebook.to(torch.float16)
+    if codebook is not None:
+        cb = codebook.to(torch.float16)
+    elif (bits, n_states) in available_codebooks():
+        cb = default_codebook(bits, n_states)
+    else:
+        cb = _synthetic_codebook(bits, seed)
     return {
         "format": 2, "n": n, "d": d, "bits": bits, "n_states": n_states, "block": block,
         "path_packed": path, "member_packed": member, "scales": scales,
