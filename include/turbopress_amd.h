@@ -42,6 +42,12 @@ int tp_abi_version(void);
 /* Static, human-readable name of a status code. */
 const char* tp_status_string(int status);
 
+/* Keep `stream` busy for about `microseconds` (<= 1e6) with a single-wave
+ * kernel that polls the GPU wall clock and always terminates.  Benchmark
+ * utility: lets a host enqueue timed work ahead of the GPU.  No reference
+ * counterpart (the reference times with host clocks, scripts/bench_packed.py). */
+int tp_device_delay(int64_t microseconds, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Trellis tables (host only, no GPU work)
  * ------------------------------------------------------------------------- */
@@ -164,6 +170,38 @@ int tp_tcq_gemv_tiled(const uint16_t* z, int64_t ldz, int64_t batch,
                       int64_t n, int64_t d, int bits, int n_states,
                       uint16_t* y, int64_t ldy, void* workspace, int64_t workspace_bytes,
                       void* stream);
+
+/* Fused PackedTCQLinear forward on the device layout: rotation of x
+ * (z = blockFWHT(x * rot_scale), Hadamard block `block`) computed per
+ * workgroup in LDS for the K range it streams, then the decode-GEMV, bias add
+ * and fp16 output, in ONE kernel launch.  x: fp16 [batch, ldx] (ldx and d
+ * multiples of 4, 8-byte aligned); other arguments as tp_tcq_gemv_tiled.
+ * Replaces turbopress/runtime.py:312-316 + 332-333 (fwht_scale, packed_gemv,
+ * bias). */
+int tp_packed_linear_forward(const uint16_t* x, int64_t ldx, int64_t batch,
+                             const uint16_t* rot_scale, int64_t block,
+                             const uint8_t* path_tiled, const uint8_t* member_tiled,
+                             const uint16_t* scales, const uint16_t* codebook,
+                             const uint16_t* bias, int64_t n, int64_t d, int bits,
+                             int n_states, uint16_t* y, int64_t ldy, void* workspace,
+                             int64_t workspace_bytes, void* stream);
+
+/* One launch for up to 4 packed linears that read the same input x (e.g. the
+ * q/k/v or gate/up projections of a decoder layer) and share one codebook:
+ * each has its own rot_scale/block, streams, scales, bias (array may be NULL),
+ * output and workspace; arrays are host arrays of n_linears entries.
+ * No reference counterpart: the reference calls PackedTCQLinear.forward once
+ * per projection (turbopress/runtime.py:304-334); this entry point serves the
+ * same calls with one launch. */
+int tp_packed_linear_forward_group(int n_linears, const uint16_t* x, int64_t ldx,
+                                   int64_t batch, const uint16_t* const* rot_scales,
+                                   const int64_t* blocks, const uint8_t* const* path_tiled,
+                                   const uint8_t* const* member_tiled,
+                                   const uint16_t* const* scales, const uint16_t* codebook,
+                                   const uint16_t* const* biases, const int64_t* ns,
+                                   int64_t d, int bits, int n_states, uint16_t* const* ys,
+                                   const int64_t* ldys, void* const* workspaces,
+                                   const int64_t* workspace_bytes, void* stream);
 
 /* Decode the device layout through the same decode path the tiled GEMV uses:
  * w[r, c] = fp16(f32(codebook[level]) * f32(scales[r])), fp16 [n, out_stride].

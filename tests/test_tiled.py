@@ -122,3 +122,54 @@ def test_graph_replays_match_eager(cuda):
             assert float((o.float() - e.float()).abs().max()) <= 2e-3 * float(e.float().abs().max()), rep
         _ = [lin(x) for lin, x in zip(lins, xs)]  # eager work between replays
         torch.cuda.synchronize()
+
+
+FUSED_CASES = [  # (n, d, bits): Hadamard block d & -d = 2, 4, 64, 512, 1024, 2048, 4096
+    (40, 130, 3), (48, 100, 2), (1536, 576, 2), (256, 2560, 3), (200, 3072, 3),
+    (300, 2048, 2), (2560, 4096, 3),
+]
+
+
+@pytest.mark.parametrize("n,d,bits", FUSED_CASES)
+@pytest.mark.parametrize("batch", [1, 4, 20])
+def test_fused_forward_matches_oracle(cuda, n, d, bits, batch):
+    """tp_packed_linear_forward: rotation computed per workgroup in LDS (full
+    blocks, partial blocks of a larger Hadamard, unaligned d fallback)."""
+    from turbopress_amd.runtime import PackedTCQLinear
+    p = make_payload(n, d, bits, 64, seed=d + batch, bias=True)
+    lin = PackedTCQLinear(p, mode="hip")
+    x = make_activation(batch, d, seed=batch)
+    y = lin(x.to(cuda)).float().cpu().numpy()
+    assert O.max_rel(y, O.tiled_forward(payload_numpy(p), x.numpy())) <= GEMV_TOL
+
+
+def test_fused_equals_two_launch_path(cuda):
+    from turbopress_amd import hip_kernel as hk
+    from turbopress_amd.runtime import PackedTCQLinear
+    p = make_payload(2560, 9728, 3, 64, seed=9)
+    lin = PackedTCQLinear(p, mode="hip")
+    x = make_activation(3, 9728, seed=9).to(cuda)
+    fused = lin(x).float()
+    two = hk.packed_gemv(hk.fwht_scale(x, lin.rot_scale, lin.block), lin).float()
+    assert float((fused - two).abs().max()) <= 2e-3 * float(two.abs().max())
+
+
+@pytest.mark.parametrize("shapes,batch", [
+    ([(1024, 2048), (1024, 1024), (1024, 1024)], 1),   # Qwen3-0.6B q/k/v
+    ([(2560, 9728), (2560, 9728)], 1),                 # Qwen3-4B gate/up
+    ([(2560, 4096), (2560, 1024), (2560, 1024)], 5),
+])
+def test_group_forward_matches_oracle(cuda, shapes, batch):
+    """tp_packed_linear_forward_group: several linears on one input, one launch."""
+    from turbopress_amd import hip_kernel as hk
+    from turbopress_amd.runtime import PackedTCQLinear
+    d = shapes[0][0]
+    payloads = [make_payload(n, dd, 3, 64, seed=60 + i, bias=(i == 1))
+                for i, (dd, n) in enumerate(shapes)]
+    lins = [PackedTCQLinear(p, mode="hip") for p in payloads]
+    x = make_activation(batch, d, seed=8)
+    outs = hk.forward_group(lins, x.to(cuda))
+    for p, o, (dd, n) in zip(payloads, outs, shapes):
+        assert o.shape == (batch, n)
+        ref = O.tiled_forward(payload_numpy(p), x.numpy())
+        assert O.max_rel(o.float().cpu().numpy(), ref) <= GEMV_TOL

@@ -163,17 +163,25 @@ struct MemberLoad3 { uint4 v; };
 // ---------------------------------------------------------------------------
 // descriptors
 // ---------------------------------------------------------------------------
+constexpr int kChunkCols = 256;                   // columns per unit (4 segments)
+constexpr int kMaxUnitsPerBlock = 2;              // K extent of one block <= 512 columns
+constexpr int kZCols = kChunkCols * kMaxUnitsPerBlock;
+constexpr int kTableBytes = kTableWords * 4;
+
 struct LinearDesc {
   const uint32_t* path;    // [T][G][16][2]
   const uint32_t* member;  // [T][G][16][MW]
-  const uint16_t* z;       // rotated activations, fp16 [batch][ldz], zero past d
+  const uint16_t* x;       // activations fp16 [batch][ldx]: unrotated (fused) or rotated z
+  const uint16_t* rs;      // rot_scale fp16 [d] (fused rotation only)
   const uint16_t* scales;  // fp16 [n]
   const uint16_t* bias;    // fp16 [n] or null
   uint16_t* y;             // fp16 [batch][ldy]
   float* ws;               // [T*16][16*NBT] fp32 split-K sums (kept zero between calls)
   uint32_t* cnt;           // [T] split-K unit counters (kept zero between calls)
-  int32_t n, T, G, G4;
-  int32_t ldz, ldy, kg, blocks;  // kg: units per block; blocks: ceil(T/8)*ceil(G4/kg)
+  float hdiv;              // fp32(sqrt(hb))
+  int32_t n, d, T, G, G4;
+  int32_t ldx, ldy, kg, blocks;  // kg: units per block; blocks: ceil(T/8)*ceil(G4/kg)
+  int32_t hb;              // Hadamard block
 };
 
 struct GemvArgs {
@@ -184,25 +192,124 @@ struct GemvArgs {
   const uint16_t* codebook;
 };
 
+// z staging in LDS: [16*NBT rows][kZCols] halves, 16-byte chunks XOR-swizzled
+// by row so that 16 batch rows reading the same column hit distinct banks.
+__device__ __forceinline__ int zl_index(int row, int col) {
+  return row * kZCols + ((((col >> 3) ^ (row & 15)) << 3) | (col & 7));
+}
+
+__device__ __forceinline__ void load4h(const uint16_t* p, float v[4]) {
+  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  v[0] = h2f((uint16_t)w.x);
+  v[1] = h2f((uint16_t)(w.x >> 16));
+  v[2] = h2f((uint16_t)w.y);
+  v[3] = h2f((uint16_t)(w.y >> 16));
+}
+
+// One 256-column chunk of z = blockFWHT(x * rs) / sqrt(hb) for batch row b,
+// computed by one wave (4 columns per lane, lane-major).  Columns >= d are
+// zero.  For hb > 256 the chunk is row block o of H_hb = H_(hb/256) (x) H_256:
+// first the signed sum of the hb/256 input chunks, then H_256.
+__device__ void rotate_chunk(const LinearDesc& L, int b, int cs, int lane, float v[4]) {
+  const int hb = L.hb;
+  const uint16_t* xr = L.x + (size_t)b * L.ldx;
+  v[0] = v[1] = v[2] = v[3] = 0.f;
+  if (hb <= kChunkCols) {
+    const int c0 = cs + lane * 4;
+    if (c0 + 3 < L.d) {
+      float xv[4], rv[4];
+      load4h(xr + c0, xv);
+      load4h(L.rs + c0, rv);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = xv[e] * rv[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c0 + e < L.d) v[e] = h2f(xr[c0 + e]) * h2f(L.rs[c0 + e]);
+    }
+  } else {
+    const int base = cs - cs % hb;
+    const int o = (cs % hb) / kChunkCols;
+    const int nsub = hb / kChunkCols;
+    for (int i = 0; i < nsub; ++i) {
+      const int c0 = base + i * kChunkCols + lane * 4;
+      float xv[4], rv[4];
+      load4h(xr + c0, xv);
+      load4h(L.rs + c0, rv);
+      const bool neg = __popc(i & o) & 1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += neg ? -(xv[e] * rv[e]) : xv[e] * rv[e];
+    }
+  }
+  const int hmax = hb < kChunkCols ? hb : kChunkCols;
+  if (hmax > 1) {
+    float a = v[0], c = v[1];
+    v[0] = a + c; v[1] = a - c;
+    a = v[2]; c = v[3];
+    v[2] = a + c; v[3] = a - c;
+  }
+  if (hmax > 2) {
+    float a = v[0], c = v[2];
+    v[0] = a + c; v[2] = a - c;
+    a = v[1]; c = v[3];
+    v[1] = a + c; v[3] = a - c;
+  }
+#pragma unroll
+  for (int sft = 0; sft < 6; ++sft) {
+    if ((4 << sft) >= hmax) break;
+    const bool upper = (lane >> sft) & 1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p = __shfl_xor(v[e], 1 << sft, 64);
+      v[e] = upper ? p - v[e] : v[e] + p;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = v[e] / L.hdiv;
+}
+
+template <bool ROT>
+__device__ void stage_z(const LinearDesc& L, int gu0, int ngu, int batch, uint16_t* zl,
+                        int wave, int lane) {
+  const int items = ngu * batch;
+  for (int it = wave; it < items; it += kWavesPerGroup) {
+    const int ci = it / batch;
+    const int b = it - ci * batch;
+    const int cs = (gu0 + ci) * kChunkCols;
+    uint2 w;
+    if constexpr (ROT) {
+      float v[4];
+      rotate_chunk(L, b, cs, lane, v);
+      w.x = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
+      w.y = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
+    } else {
+      w = *reinterpret_cast<const uint2*>(L.x + (size_t)b * L.ldx + cs + lane * 4);
+    }
+    *reinterpret_cast<uint2*>(zl + zl_index(b, ci * kChunkCols + lane * 4)) = w;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // GEMV kernel: persistent workgroups of 8 waves walk the block list; a block
-// is (8 consecutive row tiles, kg units along K); wave w takes tile w.
+// is (8 consecutive row tiles, kg <= 2 units along K); wave w takes tile w.
+// Per block the workgroup stages the block's K range of z in LDS (rotating
+// x on the fly when ROT), then every wave streams its tile.
 // ---------------------------------------------------------------------------
-template <int KB, int NS, int NBT>
+template <int KB, int NS, int NBT, bool ROT>
 __global__ void __launch_bounds__(kGroupThreads, 2)
 tcq_gemv_tiled_kernel(const GemvArgs a) {
-  __shared__ uint32_t table[kTableWords];
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  uint32_t* table = reinterpret_cast<uint32_t*>(smem);
+  uint16_t* zl = reinterpret_cast<uint16_t*>(smem + kTableBytes);
   constexpr int MW = member_words(KB);
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  build_pair_table<KB>(table, a.codebook, tid, kGroupThreads);
-  __syncthreads();
-
   const int r = lane & 15;   // A row / B,D column (batch)
   const int q = lane >> 4;   // K block of A and B, row block of D
   const uint32_t laneoff = (uint32_t)lane << 2;
   const int batch = a.batch;
+  bool table_ready = false;
 
   for (int blk = blockIdx.x; blk < a.total_blocks; blk += gridDim.x) {
     int li = 0, base = 0;
@@ -218,31 +325,42 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
     const int nkb = (L.G4 + L.kg - 1) / L.kg;
     const int tb = rel / nkb, kb = rel - tb * nkb;
     const int t = tb * kWavesPerGroup + wave;
-    if (t >= L.T) continue;
+    const bool active = t < L.T;
     const int gu0 = kb * L.kg;
     const int ngu = min(L.kg, L.G4 - gu0);
 
-    const uint32_t* pt = L.path + (size_t)t * L.G * (kTileRows * 2);
-    const uint32_t* mt = L.member + (size_t)t * L.G * (kTileRows * MW);
+    const uint32_t* pt = L.path + (size_t)(active ? t : 0) * L.G * (kTileRows * 2);
+    const uint32_t* mt = L.member + (size_t)(active ? t : 0) * L.G * (kTileRows * MW);
+
+    // Issue the block's first loads before the LDS work of this block.
+    uint32_t x1_last = 0;
+    uint2 X = {0u, 0u};
+    uint32_t Mw[MW];
+#pragma unroll
+    for (int i = 0; i < MW; ++i) Mw[i] = 0;
+    if (active) {
+      if (gu0 > 0) x1_last = pt[((4 * gu0 - 1) * kTileRows + r) * 2 + 1];
+      const int g = 4 * gu0 + q;
+      X = *reinterpret_cast<const uint2*>(pt + (g * kTileRows + r) * 2);
+#pragma unroll
+      for (int i = 0; i < MW; ++i) Mw[i] = mt[(g * kTileRows + r) * MW + i];
+    }
+    __syncthreads();  // every wave is done reading the previous block's z
+    if (!table_ready) {
+      build_pair_table<KB>(table, a.codebook, tid, kGroupThreads);
+      table_ready = true;
+    }
+    stage_z<ROT>(L, gu0, ngu, batch, zl, wave, lane);
+    __syncthreads();
+    if (!active) continue;
 
     float4_t acc[NBT];
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    // Path word X1 of the segment before this block (the lanes of the last
-    // K block hand it to the first K block of the next unit).
-    uint32_t x1_last = 0;
-    if (gu0 > 0) x1_last = pt[((4 * gu0 - 1) * kTileRows + r) * 2 + 1];
-
-    int g = 4 * gu0 + q;
-    uint2 X = *reinterpret_cast<const uint2*>(pt + (g * kTileRows + r) * 2);
-    uint32_t Mw[MW];
-#pragma unroll
-    for (int i = 0; i < MW; ++i) Mw[i] = mt[(g * kTileRows + r) * MW + i];
-
     for (int u = 0; u < ngu; ++u) {
       const int gu = gu0 + u;
-      g = 4 * gu + q;
+      const int g = 4 * gu + q;
       uint2 Xn = X;
       uint32_t Mn[MW];
 #pragma unroll
@@ -255,6 +373,7 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
       }
       // B operand: 8 halves of z per MFMA for batch column r (zero past batch).
       half8_t zb[NBT][8];
+      const int lc = (g - 4 * gu0) * kSegCols;
 #pragma unroll
       for (int bt = 0; bt < NBT; ++bt) {
         const int nb = bt * 16 + r;
@@ -262,7 +381,7 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
         for (int c = 0; c < 8; ++c) {
           const int off = (c & 4 ? 16 : 0) + (c & 2 ? 32 : 0) + (c & 1 ? 8 : 0);
           if (nb < batch)
-            zb[bt][c] = *reinterpret_cast<const half8_t*>(L.z + (size_t)nb * L.ldz + g * kSegCols + off);
+            zb[bt][c] = *reinterpret_cast<const half8_t*>(zl + zl_index(nb, lc + off));
           else
             zb[bt][c] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
         }
@@ -284,7 +403,6 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const half8_t av = __builtin_bit_cast(half8_t, A[j]);
-        // chunk index c = (x << 2) | (j >> 1) << 1 | (j & 1) with x = 0
         const int c = ((j >> 1) << 1) | (j & 1);
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt)
@@ -307,6 +425,14 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
 
     // Epilogue.  Lane holds D[4q + i][r]: rows 4q..4q+3 of the tile for batch column r.
     const int ldws = 16 * NBT;
+    const int row0 = t * kTileRows + 4 * q;
+    float sc[4], bs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = min(row0 + i, L.n - 1);
+      sc[i] = h2f(L.scales[row]);
+      bs[i] = L.bias ? h2f(L.bias[row]) : 0.f;
+    }
     if (ngu == L.G4) {
 #pragma unroll
       for (int bt = 0; bt < NBT; ++bt) {
@@ -314,40 +440,50 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
         if (nb >= batch) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int row = t * kTileRows + 4 * q + i;
-          if (row >= L.n) continue;
-          uint16_t out = f2h(acc[bt][i] * h2f(L.scales[row]));
-          if (L.bias) out = f2h(h2f(out) + h2f(L.bias[row]));
-          L.y[(size_t)nb * L.ldy + row] = out;
+          if (row0 + i >= L.n) continue;
+          uint16_t out = f2h(acc[bt][i] * sc[i]);
+          if (L.bias) out = f2h(h2f(out) + bs[i]);
+          L.y[(size_t)nb * L.ldy + row0 + i] = out;
         }
       }
     } else {
+      // Split K: partial sums travel only through device-scope read-modify-write
+      // atomics, which are performed at the point of coherence, so waiting for
+      // their completion orders them before the counter update without any
+      // cache write-back or invalidation.
 #pragma unroll
       for (int bt = 0; bt < NBT; ++bt) {
         const int nb = bt * 16 + r;
         if (nb >= batch) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          atomicAdd(L.ws + (size_t)(t * kTileRows + 4 * q + i) * ldws + bt * 16 + r, acc[bt][i]);
+          atomicAdd(L.ws + (size_t)(row0 + i) * ldws + bt * 16 + r, acc[bt][i]);
       }
-      __threadfence();
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       uint32_t old = 0;
       if (lane == 0) old = atomicAdd(L.cnt + t, (uint32_t)ngu);
       old = (uint32_t)__shfl((int)old, 0, 64);
       if (old + (uint32_t)ngu == (uint32_t)L.G4) {
-        __threadfence();
+        // Last contributor: read-and-clear the sums (also RMW atomics).
+        float v[NBT][4];
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            v[bt][i] = (bt * 16 + r < batch)
+                           ? atomicExch(L.ws + (size_t)(row0 + i) * ldws + bt * 16 + r, 0.f)
+                           : 0.f;
+        }
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) {
           const int nb = bt * 16 + r;
           if (nb >= batch) continue;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int row = t * kTileRows + 4 * q + i;
-            const float v = atomicExch(L.ws + (size_t)row * ldws + bt * 16 + r, 0.f);
-            if (row >= L.n) continue;
-            uint16_t out = f2h(v * h2f(L.scales[row]));
-            if (L.bias) out = f2h(h2f(out) + h2f(L.bias[row]));
-            L.y[(size_t)nb * L.ldy + row] = out;
+            if (row0 + i >= L.n) continue;
+            uint16_t out = f2h(v[bt][i] * sc[i]);
+            if (L.bias) out = f2h(h2f(out) + bs[i]);
+            L.y[(size_t)nb * L.ldy + row0 + i] = out;
           }
         }
         if (lane == 0) atomicExch(L.cnt + t, 0u);
@@ -584,8 +720,10 @@ namespace tp {
 struct TiledLinearArgs {
   const uint8_t* path_tiled;
   const uint8_t* member_tiled;
-  const uint16_t* z;
-  int64_t ldz;
+  const uint16_t* x;     // rotated z (rot_scale == null) or raw activations (fused rotation)
+  int64_t ldx;
+  const uint16_t* rot_scale;
+  int64_t block;         // Hadamard block (fused rotation)
   const uint16_t* scales;
   const uint16_t* bias;
   uint16_t* y;
@@ -595,9 +733,28 @@ struct TiledLinearArgs {
   int64_t workspace_bytes;
 };
 
-template <int KB, int NS, int NBT>
+constexpr size_t gemv_lds_bytes(int nbt) {
+  return (size_t)kTableBytes + (size_t)16 * nbt * kZCols * 2;
+}
+
+template <int KB, int NS, int NBT, bool ROT>
 void launch_gemv(const GemvArgs& a, int grid, hipStream_t s) {
-  hipLaunchKernelGGL((tcq_gemv_tiled_kernel<KB, NS, NBT>), dim3(grid), dim3(kGroupThreads), 0, s, a);
+  // More than 64 KiB of dynamic LDS: raise the per-kernel limit once.
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&tcq_gemv_tiled_kernel<KB, NS, NBT, ROT>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)gemv_lds_bytes(NBT));
+  (void)attr;
+  hipLaunchKernelGGL((tcq_gemv_tiled_kernel<KB, NS, NBT, ROT>), dim3(grid), dim3(kGroupThreads),
+                     gemv_lds_bytes(NBT), s, a);
+}
+
+template <int KB, int NS>
+void launch_gemv_kb(const GemvArgs& a, int grid, int nbt, bool rot, hipStream_t s) {
+  if (nbt == 1) {
+    rot ? launch_gemv<KB, NS, 1, true>(a, grid, s) : launch_gemv<KB, NS, 1, false>(a, grid, s);
+  } else {
+    rot ? launch_gemv<KB, NS, 2, true>(a, grid, s) : launch_gemv<KB, NS, 2, false>(a, grid, s);
+  }
 }
 
 int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
@@ -607,6 +764,7 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
   if (bits != 2 && bits != 3) return TP_ERR_UNSUPPORTED_BITS;
   if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
   const int nbt = batch <= 16 ? 1 : 2;
+  const bool rot = ls[0].rot_scale != nullptr;
   GemvArgs a;
   a.n_lin = n_lin;
   a.batch = (int)batch;
@@ -616,39 +774,53 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
     Geom g;
     int st = tiled_geom(ls[i].n, ls[i].d, bits, &g);
     if (st) return st;
+    if ((ls[i].rot_scale != nullptr) != rot) return TP_ERR_BAD_LAYOUT;
     units_total += g.T * g.G4;
   }
   const int cus = device_cu_count();
   const int64_t max_waves = (int64_t)cus * 2 * kWavesPerGroup;
-  // Units per block along K: spread the units over about one wave slot each.
+  int64_t kg = (units_total + max_waves - 1) / max_waves;
+  if (kg < 1) kg = 1;
+  if (kg > kMaxUnitsPerBlock) kg = kMaxUnitsPerBlock;
   int64_t total_blocks = 0;
   for (int i = 0; i < n_lin; ++i) {
     const TiledLinearArgs& l = ls[i];
-    if (!l.path_tiled || !l.member_tiled || !l.z || !l.scales || !l.y) return TP_ERR_NULL_POINTER;
+    if (!l.path_tiled || !l.member_tiled || !l.x || !l.scales || !l.y) return TP_ERR_NULL_POINTER;
     Geom g;
     tiled_geom(l.n, l.d, bits, &g);
-    if (l.ldz < g.G * kSegCols || (l.ldz & 7) || l.ldy < l.n) return TP_ERR_BAD_DIMS;
-    if (((uintptr_t)l.z & 15) || ((uintptr_t)l.path_tiled & 15) || ((uintptr_t)l.member_tiled & 15))
-      return TP_ERR_MISALIGNED;
-    int64_t kg = (units_total + max_waves - 1) / max_waves;
-    if (kg < 1) kg = 1;
-    if (kg > g.G4) kg = g.G4;
-    const int64_t nkb = (g.G4 + kg - 1) / kg;
-    const int64_t blocks = ((g.T + kWavesPerGroup - 1) / kWavesPerGroup) * nkb;
+    if (l.ldy < l.n) return TP_ERR_BAD_DIMS;
+    if (((uintptr_t)l.path_tiled & 15) || ((uintptr_t)l.member_tiled & 15)) return TP_ERR_MISALIGNED;
     LinearDesc& L = a.lin[i];
+    if (rot) {
+      const int64_t hb = l.block;
+      if (hb < 1 || (hb & (hb - 1)) || l.d % hb || hb > 16384) return TP_ERR_BAD_BLOCK;
+      if (l.ldx < l.d || (l.ldx & 3) || (l.d & 3) || ((uintptr_t)l.x & 7) || ((uintptr_t)l.rot_scale & 7))
+        return TP_ERR_MISALIGNED;
+      L.hb = (int32_t)hb;
+      L.hdiv = (float)__builtin_sqrt((double)hb);
+    } else {
+      if (l.ldx < g.G * kSegCols || (l.ldx & 7) || ((uintptr_t)l.x & 15)) return TP_ERR_BAD_DIMS;
+      L.hb = 1;
+      L.hdiv = 1.f;
+    }
+    const int64_t kgl = kg < g.G4 ? kg : g.G4;
+    const int64_t nkb = (g.G4 + kgl - 1) / kgl;
+    const int64_t blocks = ((g.T + kWavesPerGroup - 1) / kWavesPerGroup) * nkb;
     L.path = reinterpret_cast<const uint32_t*>(l.path_tiled);
     L.member = reinterpret_cast<const uint32_t*>(l.member_tiled);
-    L.z = l.z;
+    L.x = l.x;
+    L.rs = l.rot_scale;
     L.scales = l.scales;
     L.bias = l.bias;
     L.y = l.y;
     L.n = (int32_t)l.n;
+    L.d = (int32_t)l.d;
     L.T = (int32_t)g.T;
     L.G = (int32_t)g.G;
     L.G4 = (int32_t)g.G4;
-    L.ldz = (int32_t)l.ldz;
+    L.ldx = (int32_t)l.ldx;
     L.ldy = (int32_t)l.ldy;
-    L.kg = (int32_t)kg;
+    L.kg = (int32_t)kgl;
     L.blocks = (int32_t)blocks;
     if (nkb > 1) {
       const int64_t need = g.T * kTileRows * 16 * nbt * 4 + g.T * 4;
@@ -665,22 +837,20 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
   for (int i = n_lin; i < kMaxInlineLinears; ++i) a.lin[i] = a.lin[0];
   if (total_blocks > INT32_MAX) return TP_ERR_BAD_DIMS;
   a.total_blocks = (int32_t)total_blocks;
-  int grid = (int)(total_blocks < (int64_t)cus * 2 ? total_blocks : (int64_t)cus * 2);
+  const int wg_per_cu = nbt == 1 ? 2 : 1;
+  int grid = (int)(total_blocks < (int64_t)cus * wg_per_cu ? total_blocks : (int64_t)cus * wg_per_cu);
   hipStream_t s = (hipStream_t)stream;
-#define TP_GEMV(KB, NS)                                             \
-  (nbt == 1 ? launch_gemv<KB, NS, 1>(a, grid, s) : launch_gemv<KB, NS, 2>(a, grid, s))
   switch (bits * 100 + n_states) {
-    case 204: TP_GEMV(2, 4); break;
-    case 208: TP_GEMV(2, 8); break;
-    case 216: TP_GEMV(2, 16); break;
-    case 264: TP_GEMV(2, 64); break;
-    case 304: TP_GEMV(3, 4); break;
-    case 308: TP_GEMV(3, 8); break;
-    case 316: TP_GEMV(3, 16); break;
-    case 364: TP_GEMV(3, 64); break;
+    case 204: launch_gemv_kb<2, 4>(a, grid, nbt, rot, s); break;
+    case 208: launch_gemv_kb<2, 8>(a, grid, nbt, rot, s); break;
+    case 216: launch_gemv_kb<2, 16>(a, grid, nbt, rot, s); break;
+    case 264: launch_gemv_kb<2, 64>(a, grid, nbt, rot, s); break;
+    case 304: launch_gemv_kb<3, 4>(a, grid, nbt, rot, s); break;
+    case 308: launch_gemv_kb<3, 8>(a, grid, nbt, rot, s); break;
+    case 316: launch_gemv_kb<3, 16>(a, grid, nbt, rot, s); break;
+    case 364: launch_gemv_kb<3, 64>(a, grid, nbt, rot, s); break;
     default: return TP_ERR_UNSUPPORTED_STATES;
   }
-#undef TP_GEMV
   return launch_status();
 }
 
@@ -692,6 +862,43 @@ extern "C" int tp_tcq_gemv_tiled(const uint16_t* z, int64_t ldz, int64_t batch,
                                  int64_t n, int64_t d, int bits, int n_states,
                                  uint16_t* y, int64_t ldy, void* workspace, int64_t workspace_bytes,
                                  void* stream) {
-  TiledLinearArgs l{path_tiled, member_tiled, z, ldz, scales, bias, y, ldy, n, d, workspace, workspace_bytes};
+  TiledLinearArgs l{path_tiled, member_tiled, z, ldz, nullptr, 0, scales, bias, y, ldy, n, d,
+                    workspace, workspace_bytes};
   return gemv_tiled_group(&l, 1, batch, codebook, bits, n_states, stream);
+}
+
+extern "C" int tp_packed_linear_forward(const uint16_t* x, int64_t ldx, int64_t batch,
+                                        const uint16_t* rot_scale, int64_t block,
+                                        const uint8_t* path_tiled, const uint8_t* member_tiled,
+                                        const uint16_t* scales, const uint16_t* codebook,
+                                        const uint16_t* bias, int64_t n, int64_t d, int bits,
+                                        int n_states, uint16_t* y, int64_t ldy, void* workspace,
+                                        int64_t workspace_bytes, void* stream) {
+  if (!rot_scale) return TP_ERR_NULL_POINTER;
+  TiledLinearArgs l{path_tiled, member_tiled, x, ldx, rot_scale, block, scales, bias, y, ldy, n, d,
+                    workspace, workspace_bytes};
+  return gemv_tiled_group(&l, 1, batch, codebook, bits, n_states, stream);
+}
+
+extern "C" int tp_packed_linear_forward_group(int n_linears, const uint16_t* x, int64_t ldx,
+                                              int64_t batch, const uint16_t* const* rot_scales,
+                                              const int64_t* blocks, const uint8_t* const* path_tiled,
+                                              const uint8_t* const* member_tiled,
+                                              const uint16_t* const* scales, const uint16_t* codebook,
+                                              const uint16_t* const* biases, const int64_t* ns,
+                                              int64_t d, int bits, int n_states, uint16_t* const* ys,
+                                              const int64_t* ldys, void* const* workspaces,
+                                              const int64_t* workspace_bytes, void* stream) {
+  if (n_linears < 1 || n_linears > kMaxInlineLinears) return TP_ERR_BAD_DIMS;
+  if (!rot_scales || !blocks || !path_tiled || !member_tiled || !scales || !ns || !ys || !ldys ||
+      !workspaces || !workspace_bytes)
+    return TP_ERR_NULL_POINTER;
+  TiledLinearArgs ls[kMaxInlineLinears];
+  for (int i = 0; i < n_linears; ++i) {
+    if (!rot_scales[i]) return TP_ERR_NULL_POINTER;
+    ls[i] = TiledLinearArgs{path_tiled[i], member_tiled[i], x, ldx, rot_scales[i], blocks[i],
+                            scales[i], biases ? biases[i] : nullptr, ys[i], ldys[i], ns[i], d,
+                            workspaces[i], workspace_bytes[i]};
+  }
+  return gemv_tiled_group(ls, n_linears, batch, codebook, bits, n_states, stream);
 }

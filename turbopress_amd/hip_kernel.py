@@ -213,3 +213,78 @@ def gemv_tiled(zpad: Tensor, layer, bias: Tensor | None, out: Tensor) -> Tensor:
             out.data_ptr() + 2 * b0 * n, n, ws.data_ptr(), ws.numel(), stream)
         _lib.check(st, "tcq_gemv_tiled")
     return out
+
+
+def forward_tiled(layer, x: Tensor) -> Tensor:
+    """Fused rotation + decode-GEMV + bias in one launch per 32 batch rows
+    (tp_packed_linear_forward); fp16 [..., n]."""
+    _require_cuda(x, "x")
+    n, d = layer.out_features, layer.in_features
+    flat = x.reshape(-1, d).to(torch.float16).contiguous()
+    y = torch.empty(flat.shape[0], n, dtype=torch.float16, device=x.device)
+    if d % 4:
+        # Rows not 8-byte aligned: rotate into the padded layout, then GEMV.
+        zpad = rotate_padded(flat, layer.rot_scale, layer.block, layer._tiled_geo["z_cols"])
+        gemv_tiled(zpad, layer, layer.bias, y)
+        return y.reshape(*x.shape[:-1], n)
+    buf, ws = layer.tiled_packed, layer._gemv_ws
+    pb = layer._tiled_geo["path_bytes"]
+    bias = layer.bias
+    stream = current_stream_ptr(x.device)
+    lib = _lib.lib()
+    for b0 in range(0, flat.shape[0], 32):
+        nb = min(32, flat.shape[0] - b0)
+        st = lib.tp_packed_linear_forward(
+            flat.data_ptr() + 2 * b0 * d, d, nb, layer.rot_scale.data_ptr(), layer.block,
+            buf.data_ptr(), buf.data_ptr() + pb, layer.scales.data_ptr(), layer.codebook.data_ptr(),
+            0 if bias is None else bias.data_ptr(), n, d, layer.bits, layer.n_states,
+            y.data_ptr() + 2 * b0 * n, n, ws.data_ptr(), ws.numel(), stream)
+        _lib.check(st, "packed_linear_forward")
+    return y.reshape(*x.shape[:-1], n)
+
+
+def forward_group(layers, x: Tensor) -> list:
+    """One launch for up to 4 tiled layers sharing the input x and codebook
+    (tp_packed_linear_forward_group); returns their fp16 outputs."""
+    import ctypes
+    if not 1 <= len(layers) <= 4:
+        raise ValueError("forward_group takes 1 to 4 layers")
+    _require_cuda(x, "x")
+    l0 = layers[0]
+    d = l0.in_features
+    for lyr in layers:
+        if lyr.tiled_packed is None or lyr.in_features != d or lyr.bits != l0.bits \
+                or lyr.n_states != l0.n_states:
+            raise ValueError("grouped layers need the device layout and equal in_features/bits/S")
+        if not torch.equal(lyr.codebook, l0.codebook):
+            raise ValueError("grouped layers must share one codebook")
+    if d % 4:
+        return [forward_tiled(lyr, x) for lyr in layers]
+    flat = x.reshape(-1, d).to(torch.float16).contiguous()
+    k = len(layers)
+    outs = [torch.empty(flat.shape[0], lyr.out_features, dtype=torch.float16, device=x.device)
+            for lyr in layers]
+    P = ctypes.c_void_p * k
+    I = ctypes.c_int64 * k
+    stream = current_stream_ptr(x.device)
+    lib = _lib.lib()
+    for b0 in range(0, flat.shape[0], 32):
+        nb = min(32, flat.shape[0] - b0)
+        st = lib.tp_packed_linear_forward_group(
+            k, flat.data_ptr() + 2 * b0 * d, d, nb,
+            P(*[lyr.rot_scale.data_ptr() for lyr in layers]), I(*[lyr.block for lyr in layers]),
+            P(*[lyr.tiled_packed.data_ptr() for lyr in layers]),
+            P(*[lyr.tiled_packed.data_ptr() + lyr._tiled_geo["path_bytes"] for lyr in layers]),
+            P(*[lyr.scales.data_ptr() for lyr in layers]), l0.codebook.data_ptr(),
+            P(*[0 if lyr.bias is None else lyr.bias.data_ptr() for lyr in layers]),
+            I(*[lyr.out_features for lyr in layers]), d, l0.bits, l0.n_states,
+            P(*[o.data_ptr() + 2 * b0 * o.shape[1] for o in outs]), I(*[o.shape[1] for o in outs]),
+            P(*[lyr._gemv_ws.data_ptr() for lyr in layers]), I(*[lyr._gemv_ws.numel() for lyr in layers]),
+            stream)
+        _lib.check(st, "packed_linear_forward_group")
+    return [o.reshape(*x.shape[:-1], o.shape[1]) for o in outs]
+
+
+def device_delay(microseconds: int, device=None) -> None:
+    """Enqueue a bounded busy-wait kernel on the current stream (benchmarks)."""
+    _lib.check(_lib.lib().tp_device_delay(int(microseconds), current_stream_ptr(device)), "device_delay")

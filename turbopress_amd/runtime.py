@@ -183,10 +183,7 @@ class PackedTCQLinear(nn.Module):
                 y = y + self.bias
             return y.to(x.dtype)
         if self.tiled_packed is not None:
-            zpad = hk.rotate_padded(x, self.rot_scale, self.block, self._tiled_geo["z_cols"])
-            y = torch.empty(zpad.shape[0], self.out_features, dtype=torch.float16, device=x.device)
-            hk.gemv_tiled(zpad, self, self.bias, y)
-            return y.reshape(*x.shape[:-1], self.out_features).to(x.dtype)
+            return hk.forward_tiled(self, x).to(x.dtype)
         z = hk.fwht_scale(x, self.rot_scale, self.block)
         if self.mode == "hip":
             y = hk.packed_gemv(z, self, bias=self.bias)
