@@ -3,25 +3,32 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-seconds S]
 
 Workload: the 7 projections (q, k, v, o, gate, up,
-down) of each of Qwen3-4B's 36 decoder layers, as 252 distinct packed linears
-(k = 3 bits/weight, S = 64 trellis states, seeded synthetic streams and
-activations), all captured in one HIP graph and replayed once per step.  The
-weights (1.37 GB) exceed the 256 MB Infinity Cache, so each replay streams
-them from HBM.
+down) of each of Qwen3-4B's 36 decoder layers -- 252 distinct packed linears
+at k = 3 bits/weight, S = 64 trellis states, seeded synthetic streams -- with
+seeded fp16 activations (N(0,1), 1 % of channels x20), one input per
+shared-input group (q/k/v, o, gate/up, down) of every layer.  The weights
+(1.37 GB) exceed the 256 MB Infinity Cache, so every step streams them from
+HBM.  A step is captured once in a HIP graph and replayed; K replays are
+timed with HIP events between two device synchronisations.
 
-Prints ONE JSON line: ``value`` is µs per decode step (lower is better), with
-the step's algorithmic GB/s and % of MI355X's 8 TB/s HBM peak; ``roofline``
-covers the dominant kernel (the gate/up-shaped decode-GEMV, timed per launch
-with HIP events over 36 distinct weight sets on the stream it runs on), and
-``cpu_baseline`` times the reference's CPU tiled path (the oracle's op-for-op
-restatement) on a bounded sample on this host.
+``value`` (µs per step, lower is better) is the primary executor: one
+persistent launch for all 252 linears (tp_stack_run) with the decoder's data
+dependencies enforced on the device -- every linear of phase p (q/k/v | o |
+gate/up | down of each layer, 144 phases) waits for all of phase p-1.  The
+line also reports the same step without the ordering, with one launch per
+shared-input group (144 launches) and with one launch per linear (252
+launches, the drop-in PackedTCQLinear.forward path).
+
+``roofline`` covers the dominant kernel (the stack kernel: one launch per
+step moves the whole step's algorithmic bytes); ``cpu_baseline`` times the
+reference's CPU tiled path (the oracle's op-for-op restatement) on a bounded
+sample on this host.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -33,6 +40,9 @@ N_LAYERS = 36
 BITS = 3
 N_STATES = 64
 BATCH = 1
+ORDER = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+GROUP_INPUT = {"q_proj": "attn", "k_proj": "attn", "v_proj": "attn", "o_proj": "o",
+               "gate_proj": "mlp", "up_proj": "mlp", "down_proj": "down"}
 
 
 def _bytes(n: int, d: int, bits: int, batch: int) -> int:
@@ -40,46 +50,49 @@ def _bytes(n: int, d: int, bits: int, batch: int) -> int:
     return n * d * bits // 8 + 2 * n + 2 * (1 << (bits + 1)) + 2 * d + 2 * batch * d + 2 * batch * n
 
 
-def build_stack(device, n_layers=N_LAYERS, bits=BITS):
+def build_layers(device, n_layers=N_LAYERS, bits=BITS, batch=BATCH):
     from turbopress_amd.runtime import PackedTCQLinear
     from turbopress_amd.synthetic import QWEN3_4B_LAYER, make_activation, make_payload
-    layers = []
+    layers, inputs = [], []
     for li in range(n_layers):
         mods = {}
-        for j, (name, (d, n)) in enumerate(QWEN3_4B_LAYER.items()):
-            seed = 1000 * li + j
-            mods[name] = (PackedTCQLinear(make_payload(n, d, bits, N_STATES, seed=seed), mode="hip"),
-                          make_activation(BATCH, d, seed=seed).to(device))
+        for j, name in enumerate(ORDER):
+            d, n = QWEN3_4B_LAYER[name]
+            mods[name] = PackedTCQLinear(make_payload(n, d, bits, N_STATES, seed=1000 * li + j), mode="hip")
+        xs = {}
+        for k, g in enumerate(("attn", "o", "mlp", "down")):
+            d = {"attn": 2560, "o": 4096, "mlp": 2560, "down": 9728}[g]
+            xs[g] = make_activation(batch, d, seed=1000 * li + 100 + k).to(device)
         layers.append(mods)
-    return layers
+        inputs.append(xs)
+    return layers, inputs
 
 
-def step_bytes(layers) -> int:
-    return sum(_bytes(m.out_features, m.in_features, m.bits, BATCH)
-               for mods in layers for (m, _) in mods.values())
+def step_bytes(layers, batch=BATCH) -> int:
+    return sum(_bytes(m.out_features, m.in_features, m.bits, batch) for mods in layers for m in mods.values())
 
 
-def run_step(layers, outs):
-    i = 0
-    for mods in layers:
-        for name in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
-            m, x = mods[name]
-            outs[i] = m(x)
-            i += 1
+def make_stack(layers, inputs, ordered):
+    from turbopress_amd.decode_step import QWEN_PHASES, LinearStack
+    entries = []
+    for li, (mods, xs) in enumerate(zip(layers, inputs)):
+        for name in ORDER:
+            entries.append((mods[name], xs[GROUP_INPUT[name]], 4 * li + QWEN_PHASES[name]))
+    return LinearStack(entries, ordered=ordered)
 
 
-def time_graph(layers, steps, warmup):
-    outs = [None] * (7 * len(layers))
+def time_graph(step_fn, steps, warmup):
+    """Capture step_fn once, replay `warmup` times, then time `steps` replays
+    between device synchronisations.  Returns ms per step (events, wall)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
-        for _ in range(max(warmup, 1)):
-            run_step(layers, outs)
+        step_fn()
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        run_step(layers, outs)
+        step_fn()
     for _ in range(warmup):
         g.replay()
     torch.cuda.synchronize()
@@ -91,34 +104,7 @@ def time_graph(layers, steps, warmup):
     end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return start.elapsed_time(end) / steps, wall / steps * 1e3, g, outs
-
-
-def time_dominant_kernel(layers, reps=3):
-    """Per-launch HIP-event timing of the gate-shaped GEMV (9728 x 2560) over the
-    36 layers' distinct weights, on the stream the kernel is launched on."""
-    from turbopress_amd import hip_kernel as hk
-    stream = torch.cuda.current_stream()
-    zs = []
-    for mods in layers:
-        m, x = mods["gate_proj"]
-        zs.append((m, hk.fwht_scale(x, m.rot_scale, m.block)))
-    for m, z in zs:  # warm
-        hk.packed_gemv(z, m)
-    torch.cuda.synchronize()
-    evs = []
-    for _ in range(reps):
-        for m, z in zs:
-            a = torch.cuda.Event(enable_timing=True)
-            b = torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            hk.packed_gemv(z, m)
-            b.record(stream)
-            evs.append((a, b))
-    torch.cuda.synchronize()
-    ms = [a.elapsed_time(b) for a, b in evs]
-    m0 = zs[0][0]
-    return sum(ms) / len(ms), _bytes(m0.out_features, m0.in_features, m0.bits, BATCH)
+    return start.elapsed_time(end) / steps, wall / steps * 1e3, g
 
 
 def cpu_baseline(budget_s: float):
@@ -129,7 +115,8 @@ def cpu_baseline(budget_s: float):
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
     mods = []
-    for j, (name, (d, n)) in enumerate(QWEN3_4B_LAYER.items()):
+    for j, name in enumerate(ORDER):
+        d, n = QWEN3_4B_LAYER[name]
         mods.append((TiledLinearCPU(make_payload(n, d, BITS, N_STATES, seed=j)),
                      make_activation(BATCH, d, seed=j)))
     times = []
@@ -159,27 +146,55 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only-primary", action="store_true", help="skip the comparison executors")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: the packed-TCQ decode path is built and measured "
               "on a single GPU only (multi-GPU sharding is design-only); run with --gpus 1.",
               file=sys.stderr)
         return 2
+    from turbopress_amd import decode_step
+
     torch.manual_seed(0)
     dev = torch.device("cuda", 0)
-    print(f"[bench] building {N_LAYERS}x7 packed linears (k={BITS}, S={N_STATES})", file=sys.stderr, flush=True)
-    layers = build_stack(dev)
+    log = lambda m: print(f"[bench] {m}", file=sys.stderr, flush=True)  # noqa: E731
+    log(f"building {N_LAYERS}x7 packed linears (k={BITS}, S={N_STATES}, batch {BATCH})")
+    layers, inputs = build_layers(dev)
     nbytes = step_bytes(layers)
-    print(f"[bench] capturing graph; {nbytes / 1e9:.4f} GB per step", file=sys.stderr, flush=True)
-    ms_ev, ms_wall, _, _ = time_graph(layers, args.steps, args.warmup)
-    ms = ms_ev
-    print(f"[bench] graph step {ms * 1e3:.1f} us (wall {ms_wall * 1e3:.1f} us)", file=sys.stderr, flush=True)
-    dom_ms, dom_bytes = time_dominant_kernel(layers)
-    achieved = dom_bytes / (dom_ms * 1e-3) / 1e9
-    print(f"[bench] dominant kernel {dom_ms * 1e3:.2f} us/launch, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
+    log(f"{nbytes / 1e9:.4f} GB per step")
+
+    stack_o = make_stack(layers, inputs, ordered=True)
+    ms, ms_wall, _ = time_graph(stack_o.run, args.steps, args.warmup)
+    if stack_o.error():
+        raise RuntimeError("stack phase wait timed out")
+    log(f"stack (ordered, 1 launch): {ms * 1e3:.1f} us/step")
+    extra = {}
+    if not args.only_primary:
+        stack_u = make_stack(layers, inputs, ordered=False)
+        ms_u, _, _ = time_graph(stack_u.run, args.steps, args.warmup)
+        log(f"stack (unordered, 1 launch): {ms_u * 1e3:.1f} us/step")
+        steps_slow = max(5, args.steps // 5)
+
+        def grouped():
+            for mods, xs in zip(layers, inputs):
+                decode_step.layer_forward(mods, xs)
+
+        ms_g, _, _ = time_graph(grouped, steps_slow, 2)
+        log(f"grouped launches (144/step): {ms_g * 1e3:.1f} us/step")
+
+        def per_linear():
+            for mods, xs in zip(layers, inputs):
+                for name in ORDER:
+                    mods[name](xs[GROUP_INPUT[name]])
+
+        ms_p, _, _ = time_graph(per_linear, steps_slow, 2)
+        log(f"per-linear launches (252/step): {ms_p * 1e3:.1f} us/step")
+        extra = {"unordered_stack_us": round(ms_u * 1e3, 2), "grouped_launches_us": round(ms_g * 1e3, 2),
+                 "per_linear_launches_us": round(ms_p * 1e3, 2)}
+
     cpu = None
     if not args.no_cpu_baseline:
-        print("[bench] CPU baseline", file=sys.stderr, flush=True)
+        log("CPU baseline")
         cpu = cpu_baseline(args.cpu_seconds)
     gbps = nbytes / (ms * 1e-3) / 1e9
     line = {
@@ -187,16 +202,18 @@ def main() -> int:
         "value": round(ms * 1e3, 2), "unit": "us/step", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp16", "data": "synthetic",
+        "dtype": "fp16", "data": "synthetic (seeded codes, codebook, scales, signs, activations)",
         "config": {"workload": "qwen3-4b decode-step linear stack: 36 layers x (q,k,v,o,gate,up,down), "
-                               "one HIP graph", "layers": N_LAYERS, "bits": BITS, "n_states": N_STATES,
-                   "batch": BATCH, "bytes_per_step": nbytes},
+                               "one HIP graph, one persistent launch, phases q/k/v->o->gate/up->down "
+                               "enforced on device", "layers": N_LAYERS, "bits": BITS,
+                   "n_states": N_STATES, "batch": BATCH, "bytes_per_step": nbytes},
         "gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
         "wall_ms_per_step": round(ms_wall, 5),
-        "roofline": {"kernel": "tcq decode-GEMV, gate/up shape 9728x2560 k=3 B=1",
-                     "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "us_per_launch": round(dom_ms * 1e3, 3), "bytes_per_launch": dom_bytes},
+        "roofline": {"kernel": "tcq_stack_kernel<3,64,1> (all 252 linears, one launch per step)",
+                     "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "us_per_launch": round(ms * 1e3, 2), "bytes_per_launch": nbytes},
+        "executors": extra,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -203,6 +203,59 @@ int tp_packed_linear_forward_group(int n_linears, const uint16_t* x, int64_t ldx
                                    const int64_t* ldys, void* const* workspaces,
                                    const int64_t* workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Decode-step stack: every packed linear of a step in one persistent launch
+ * ------------------------------------------------------------------------- */
+
+/* One linear of a stack (host struct; pointers are device pointers). */
+typedef struct tp_stack_linear {
+  const uint8_t* path_tiled;    /* device layout, from tp_retile */
+  const uint8_t* member_tiled;
+  const uint16_t* x;            /* fp16 [batch, ldx] input of this linear (ldx, d multiples of 4) */
+  int64_t ldx;
+  const uint16_t* rot_scale;    /* fp16 [d] */
+  int64_t block;                /* Hadamard block */
+  const uint16_t* scales;       /* fp16 [n] */
+  const uint16_t* bias;         /* fp16 [n] or NULL */
+  uint16_t* y;                  /* fp16 [batch, ldy] output */
+  int64_t ldy;
+  int64_t n, d;
+  int32_t phase;                /* dependency phase, non-decreasing along the list */
+  int32_t reserved;
+} tp_stack_linear;
+
+/* Bytes of the device plan for n_linears linears in n_phases phases (0 when
+ * invalid).  Host only. */
+int64_t tp_stack_plan_bytes(int n_linears, int n_phases);
+
+/* Validate the linears and write the plan (descriptors, block prefix sums,
+ * phase tables, zeroed counters, batch in [1, 32]) into `plan` (device
+ * memory, 256-byte aligned) with a blocking copy.  Setup call, not capturable.  bits in {2, 3}.
+ * No reference counterpart: the reference has no step-level executor; this
+ * serves the decode step of scripts/graph_decode_bench.py:70-118. */
+int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears, int bits,
+                       int64_t batch, void* plan, int64_t plan_bytes);
+
+/* Run every linear of the plan (y = PackedTCQLinear.forward(x) for each, as
+ * tp_packed_linear_forward computes it) in ONE persistent launch.  With
+ * ordered != 0 a linear of phase p starts only after all linears of phase
+ * p-1 finished.  The plan's counters return to zero after each run, so one
+ * plan serves any number of runs or graph replays on one stream (runs that
+ * overlap on one plan race).  Sizes are read from the plan; `batch` (the
+ * plan's batch) and total_blocks (tp_stack_plan_blocks) only size the launch.
+ * A launch whose batch tiles cannot hold the plan's batch sets error 2 and
+ * does nothing. */
+int tp_stack_run(void* plan, int64_t batch, const uint16_t* codebook, int bits,
+                 int n_states, int ordered, int64_t total_blocks, void* stream);
+
+/* Work blocks of a stack of linears with the given (n) sizes: sum of
+ * ceil(ceil(n/16)/8).  Host only. */
+int64_t tp_stack_plan_blocks(const int64_t* ns, int n_linears);
+
+/* Copy the plan's error flag (1 = a phase wait timed out, 2 = batch mismatch) to *error_out
+ * (blocking).  Not capturable. */
+int tp_stack_error(const void* plan, int* error_out);
+
 /* Decode the device layout through the same decode path the tiled GEMV uses:
  * w[r, c] = fp16(f32(codebook[level]) * f32(scales[r])), fp16 [n, out_stride].
  * bits in {2, 3}.  The bit-exact check of the bandwidth path.

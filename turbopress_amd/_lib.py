@@ -52,6 +52,24 @@ SIGNATURES: dict[str, tuple] = {
                                                _I64, c_int, c_int, _P, _P, _P, _P, _P]),
 }
 
+class StackLinear(ctypes.Structure):
+    """tp_stack_linear (include/turbopress_amd.h)."""
+    _fields_ = [
+        ("path_tiled", c_void_p), ("member_tiled", c_void_p),
+        ("x", c_void_p), ("ldx", c_int64), ("rot_scale", c_void_p), ("block", c_int64),
+        ("scales", c_void_p), ("bias", c_void_p), ("y", c_void_p), ("ldy", c_int64),
+        ("n", c_int64), ("d", c_int64), ("phase", ctypes.c_int32), ("reserved", ctypes.c_int32),
+    ]
+
+
+SIGNATURES.update({
+    "tp_stack_plan_bytes": (c_int64, [c_int, c_int]),
+    "tp_stack_plan_init": (c_int, [POINTER(StackLinear), c_int, c_int, _I64, _P, _I64]),
+    "tp_stack_run": (c_int, [_P, _I64, _P, c_int, c_int, c_int, _I64, _P]),
+    "tp_stack_plan_blocks": (c_int64, [POINTER(c_int64), c_int]),
+    "tp_stack_error": (c_int, [_P, POINTER(c_int)]),
+})
+
 _LIB: ctypes.CDLL | None = None
 _LOAD_ERROR: str | None = None
 

@@ -1,0 +1,470 @@
+// Device code shared by the tiled decode-GEMV kernels (tp_tiled.hip: one to
+// four linears per launch; tp_stack.hip: every linear of a decode step in one
+// persistent launch).  See tp_tiled.hip for the device layout.
+#pragma once
+
+#include "tp_common.h"
+
+#include <cstdlib>
+
+namespace tp {
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kTileRows = 16;
+constexpr int kSegCols = 64;
+constexpr int kWavesPerGroup = 8;                 // waves per workgroup
+constexpr int kGroupThreads = 64 * kWavesPerGroup;
+constexpr int kTableWords = 256 * 64;            // 64 KiB
+constexpr int kMaxInlineLinears = 4;
+
+__host__ __device__ constexpr int member_words(int bits) {
+  return bits == 2 ? 2 : bits == 3 ? 4 : bits == 4 ? 6 : 0;
+}
+
+// Delay mask of a window-coordinate generator: bit t set when the subset bit
+// XORs in the path bit t columns back.
+__host__ __device__ constexpr uint32_t delay_mask(uint32_t g, int m) {
+  uint32_t gw = ((g >> m) & 1u) << m;
+  for (int j = 0; j < m; ++j) gw |= ((g >> (m - 1 - j)) & 1u) << j;
+  uint32_t dm = 0;
+  for (int j = 0; j <= m; ++j)
+    if ((gw >> j) & 1u) dm |= 1u << (m - j);
+  return dm;
+}
+
+template <int NS> struct TrellisOf;
+template <> struct TrellisOf<4> { static constexpr int m = 2; static constexpr uint32_t g0 = 05, g1 = 07; };
+template <> struct TrellisOf<8> { static constexpr int m = 3; static constexpr uint32_t g0 = 015, g1 = 017; };
+template <> struct TrellisOf<16> { static constexpr int m = 4; static constexpr uint32_t g0 = 023, g1 = 035; };
+template <> struct TrellisOf<64> { static constexpr int m = 6; static constexpr uint32_t g0 = 0133, g1 = 0171; };
+
+// Subset words of the two 16-weight groups carried by one interleaved path word.
+// SA bit 2j / 2j+1 = subset bit 0 / 1 of first-half weight j; SB likewise for
+// the second half.  `prev` is the interleaved word of the 16 preceding columns
+// of each half.
+template <int NS>
+__device__ __forceinline__ void subset_words(uint32_t cur, uint32_t prev, uint32_t& SA, uint32_t& SB) {
+  constexpr int m = TrellisOf<NS>::m;
+  constexpr uint32_t D0 = delay_mask(TrellisOf<NS>::g0, m);
+  constexpr uint32_t D1 = delay_mask(TrellisOf<NS>::g1, m);
+  uint32_t e0 = (D0 & 1u) ? cur : 0u;
+  uint32_t e1 = (D1 & 1u) ? cur : 0u;
+#pragma unroll
+  for (int t = 1; t <= m; ++t) {
+    const uint32_t a = __builtin_amdgcn_alignbit(cur, prev, 32 - 2 * t);
+    if ((D0 >> t) & 1u) e0 ^= a;
+    if ((D1 >> t) & 1u) e1 ^= a;
+  }
+  SA = (e0 & 0x55555555u) | ((e1 << 1) & 0xAAAAAAAAu);
+  SB = ((e0 >> 1) & 0x55555555u) | (e1 & 0xAAAAAAAAu);
+}
+
+// LDS byte address of the lane's copy of table entry `byte b of idx`.
+__device__ __forceinline__ uint32_t table_addr(uint32_t idx, uint32_t laneoff, int b) {
+  return __builtin_amdgcn_perm(idx, laneoff, 0x0C0C0000u | ((4u + b) << 8));
+}
+
+__device__ __forceinline__ uint32_t lds_word(const uint32_t* table, uint32_t byte_addr) {
+  return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(table) + byte_addr);
+}
+
+// Member words consumed with one interleaved path word (x = 0 or 1).
+template <int KB> struct MemberWords;
+template <> struct MemberWords<2> { uint32_t w; };
+template <> struct MemberWords<3> { uint32_t a, b; };
+
+// Decode 32 weights (16 of each half) of one lane into four MFMA A operands:
+// A[0]/A[1] = first-half columns 0-7 / 8-15, A[2]/A[3] = second half.
+template <int KB, int NS>
+__device__ __forceinline__ void decode_word(uint32_t cur, uint32_t prev, const MemberWords<KB>& M,
+                                            const uint32_t* table, uint32_t laneoff, u32x4_t A[4]) {
+  uint32_t SA, SB;
+  subset_words<NS>(cur, prev, SA, SB);
+  uint32_t iae, iao, ibe, ibo;
+  if constexpr (KB == 3) {
+    iae = (SA & 0x0F0F0F0Fu) | ((M.a << 4) & 0xF0F0F0F0u);
+    iao = ((SA >> 4) & 0x0F0F0F0Fu) | (M.a & 0xF0F0F0F0u);
+    ibe = (SB & 0x0F0F0F0Fu) | ((M.b << 4) & 0xF0F0F0F0u);
+    ibo = ((SB >> 4) & 0x0F0F0F0Fu) | (M.b & 0xF0F0F0F0u);
+  } else {
+    iae = (SA & 0x0F0F0F0Fu) | ((M.w << 4) & 0xF0F0F0F0u);
+    iao = ((SA >> 4) & 0x0F0F0F0Fu) | (M.w & 0xF0F0F0F0u);
+    ibe = (SB & 0x0F0F0F0Fu) | ((M.w << 2) & 0xF0F0F0F0u);
+    ibo = ((SB >> 4) & 0x0F0F0F0Fu) | ((M.w >> 2) & 0xF0F0F0F0u);
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    A[0][2 * h] = lds_word(table, table_addr(iae, laneoff, h));
+    A[0][2 * h + 1] = lds_word(table, table_addr(iao, laneoff, h));
+    A[1][2 * h] = lds_word(table, table_addr(iae, laneoff, 2 + h));
+    A[1][2 * h + 1] = lds_word(table, table_addr(iao, laneoff, 2 + h));
+    A[2][2 * h] = lds_word(table, table_addr(ibe, laneoff, h));
+    A[2][2 * h + 1] = lds_word(table, table_addr(ibo, laneoff, h));
+    A[3][2 * h] = lds_word(table, table_addr(ibe, laneoff, 2 + h));
+    A[3][2 * h + 1] = lds_word(table, table_addr(ibo, laneoff, 2 + h));
+  }
+}
+
+// Pair table: entry v = (cb[level_a] | cb[level_b] << 16), with the index byte
+// v = [S0a S1a S0b S1b | member bits], replicated in 64 lane copies.
+template <int KB>
+__device__ __forceinline__ uint32_t pair_entry(const uint16_t* cb, uint32_t v) {
+  const uint32_t sa = v & 3u, sb = (v >> 2) & 3u;
+  uint32_t ma, mb;
+  if constexpr (KB == 3) {
+    ma = (v >> 4) & 3u;
+    mb = (v >> 6) & 3u;
+  } else {
+    ma = (v >> 4) & 1u;
+    mb = (v >> 5) & 1u;
+  }
+  return (uint32_t)cb[ma * 4 + sa] | ((uint32_t)cb[mb * 4 + sb] << 16);
+}
+
+template <int KB>
+__device__ void build_pair_table(uint32_t* table, const uint16_t* cb, int tid, int nthreads) {
+  // Each thread writes 16-byte runs (4 lane copies) of one entry.
+  for (int i = tid; i < kTableWords / 4; i += nthreads) {
+    const uint32_t v = (uint32_t)(i >> 4);  // 16 runs of 4 copies per entry
+    const uint32_t e = pair_entry<KB>(cb, v);
+    u32x4_t run = {e, e, e, e};
+    *reinterpret_cast<u32x4_t*>(table + 4 * i) = run;
+  }
+}
+
+// Same table from a codebook held one entry per lane (lane l has cb[l % 2^(KB+1)]):
+// no memory reads, entries gathered with lane shuffles.
+template <int KB>
+__device__ void build_pair_table_lanes(uint32_t* table, uint32_t cb_lane, int tid, int nthreads) {
+  for (int i = tid; i < kTableWords / 4; i += nthreads) {
+    const uint32_t v = (uint32_t)(i >> 4);
+    const uint32_t sa = v & 3u, sb = (v >> 2) & 3u;
+    uint32_t ma, mb;
+    if constexpr (KB == 3) {
+      ma = (v >> 4) & 3u;
+      mb = (v >> 6) & 3u;
+    } else {
+      ma = (v >> 4) & 1u;
+      mb = (v >> 5) & 1u;
+    }
+    const uint32_t lo = (uint32_t)__shfl((int)cb_lane, (int)(ma * 4 + sa), 64);
+    const uint32_t hi = (uint32_t)__shfl((int)cb_lane, (int)(mb * 4 + sb), 64);
+    const uint32_t e = (lo & 0xFFFFu) | (hi << 16);
+    u32x4_t run = {e, e, e, e};
+    *reinterpret_cast<u32x4_t*>(table + 4 * i) = run;
+  }
+}
+
+struct MemberLoad2 { uint2 v; };
+struct MemberLoad3 { uint4 v; };
+
+// ---------------------------------------------------------------------------
+// descriptors
+// ---------------------------------------------------------------------------
+constexpr int kChunkCols = 256;                   // columns per unit (4 segments)
+constexpr int kMaxUnitsPerBlock = 2;              // K extent of one block <= 512 columns
+constexpr int kZCols = kChunkCols * kMaxUnitsPerBlock;
+constexpr int kTableBytes = kTableWords * 4;
+
+struct LinearDesc {
+  const uint32_t* path;    // [T][G][16][2]
+  const uint32_t* member;  // [T][G][16][MW]
+  const uint16_t* x;       // activations fp16 [batch][ldx]: unrotated (fused) or rotated z
+  const uint16_t* rs;      // rot_scale fp16 [d] (fused rotation only)
+  const uint16_t* scales;  // fp16 [n]
+  const uint16_t* bias;    // fp16 [n] or null
+  uint16_t* y;             // fp16 [batch][ldy]
+  float* ws;               // [T*16][16*NBT] fp32 split-K sums (kept zero between calls)
+  uint32_t* cnt;           // [T] split-K unit counters (kept zero between calls)
+  float hdiv;              // fp32(sqrt(hb))
+  int32_t n, d, T, G, G4;
+  int32_t ldx, ldy, kg, blocks;  // kg: units per block; blocks: ceil(T/8)*ceil(G4/kg)
+  int32_t hb;              // Hadamard block
+};
+
+
+// z staging in LDS: [16*NBT rows][kZCols] halves, 16-byte chunks XOR-swizzled
+// by row so that 16 batch rows reading the same column hit distinct banks.
+__device__ __forceinline__ int zl_index(int row, int col) {
+  return row * kZCols + ((((col >> 3) ^ (row & 15)) << 3) | (col & 7));
+}
+
+__device__ __forceinline__ void load4h(const uint16_t* p, float v[4]) {
+  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  v[0] = h2f((uint16_t)w.x);
+  v[1] = h2f((uint16_t)(w.x >> 16));
+  v[2] = h2f((uint16_t)w.y);
+  v[3] = h2f((uint16_t)(w.y >> 16));
+}
+
+// One 256-column chunk of z = blockFWHT(x * rs) / sqrt(hb) for batch row b,
+// computed by one wave (4 columns per lane, lane-major).  Columns >= d are
+// zero.  For hb > 256 the chunk is row block o of H_hb = H_(hb/256) (x) H_256:
+// first the signed sum of the hb/256 input chunks, then H_256.
+__device__ void rotate_chunk(const LinearDesc& L, int b, int cs, int lane, float v[4]) {
+  const int hb = L.hb;
+  const uint16_t* xr = L.x + (size_t)b * L.ldx;
+  v[0] = v[1] = v[2] = v[3] = 0.f;
+  if (hb <= kChunkCols) {
+    const int c0 = cs + lane * 4;
+    if (c0 + 3 < L.d) {
+      float xv[4], rv[4];
+      load4h(xr + c0, xv);
+      load4h(L.rs + c0, rv);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = xv[e] * rv[e];
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        if (c0 + e < L.d) v[e] = h2f(xr[c0 + e]) * h2f(L.rs[c0 + e]);
+    }
+  } else {
+    const int base = cs - cs % hb;
+    const int o = (cs % hb) / kChunkCols;
+    const int nsub = hb / kChunkCols;
+    for (int i = 0; i < nsub; ++i) {
+      const int c0 = base + i * kChunkCols + lane * 4;
+      float xv[4], rv[4];
+      load4h(xr + c0, xv);
+      load4h(L.rs + c0, rv);
+      const bool neg = __popc(i & o) & 1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += neg ? -(xv[e] * rv[e]) : xv[e] * rv[e];
+    }
+  }
+  const int hmax = hb < kChunkCols ? hb : kChunkCols;
+  if (hmax > 1) {
+    float a = v[0], c = v[1];
+    v[0] = a + c; v[1] = a - c;
+    a = v[2]; c = v[3];
+    v[2] = a + c; v[3] = a - c;
+  }
+  if (hmax > 2) {
+    float a = v[0], c = v[2];
+    v[0] = a + c; v[2] = a - c;
+    a = v[1]; c = v[3];
+    v[1] = a + c; v[3] = a - c;
+  }
+#pragma unroll
+  for (int sft = 0; sft < 6; ++sft) {
+    if ((4 << sft) >= hmax) break;
+    const bool upper = (lane >> sft) & 1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p = __shfl_xor(v[e], 1 << sft, 64);
+      v[e] = upper ? p - v[e] : v[e] + p;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = v[e] / L.hdiv;
+}
+
+// Activations of one staging item loaded ahead of the block's LDS work: the
+// common small case (at most one item per wave, Hadamard block <= 512) keeps
+// every load of the block in flight before the first barrier.
+struct ZPrefetch {
+  bool valid;
+  uint2 x0, r0, x1, r1;
+};
+
+template <bool ROT>
+__device__ __forceinline__ void prefetch_z(const LinearDesc& L, int gu0, int ngu, int batch,
+                                           int wave, int lane, ZPrefetch& zp) {
+  zp.valid = false;
+  const int items = ngu * batch;
+  if (items > kWavesPerGroup || wave >= items || (ROT && L.hb > 2 * kChunkCols)) return;
+  const int ci = wave / batch, b = wave - ci * batch;
+  const int cs = (gu0 + ci) * kChunkCols;
+  zp.valid = true;
+  zp.x0 = zp.r0 = zp.x1 = zp.r1 = uint2{0u, 0u};
+  if constexpr (ROT) {
+    const uint16_t* xr = L.x + (size_t)b * L.ldx;
+    if (L.hb <= kChunkCols) {
+      const int c0 = cs + lane * 4;
+      if (c0 < L.d) {
+        zp.x0 = *reinterpret_cast<const uint2*>(xr + c0);
+        zp.r0 = *reinterpret_cast<const uint2*>(L.rs + c0);
+      }
+    } else {
+      const int c0 = cs - cs % L.hb + lane * 4;
+      zp.x0 = *reinterpret_cast<const uint2*>(xr + c0);
+      zp.r0 = *reinterpret_cast<const uint2*>(L.rs + c0);
+      zp.x1 = *reinterpret_cast<const uint2*>(xr + c0 + kChunkCols);
+      zp.r1 = *reinterpret_cast<const uint2*>(L.rs + c0 + kChunkCols);
+    }
+  } else {
+    zp.x0 = *reinterpret_cast<const uint2*>(L.x + (size_t)b * L.ldx + cs + lane * 4);
+  }
+}
+
+__device__ __forceinline__ void unpack4h(uint2 w, float v[4]) {
+  v[0] = h2f((uint16_t)w.x);
+  v[1] = h2f((uint16_t)(w.x >> 16));
+  v[2] = h2f((uint16_t)w.y);
+  v[3] = h2f((uint16_t)(w.y >> 16));
+}
+
+// H_256 (or H_hb for hb < 256) butterflies over a lane-major chunk, then 1/sqrt(hb).
+__device__ __forceinline__ void chunk_fwht(const LinearDesc& L, int lane, float v[4]) {
+  const int hb = L.hb;
+  const int hmax = hb < kChunkCols ? hb : kChunkCols;
+  if (hmax > 1) {
+    float a = v[0], c = v[1];
+    v[0] = a + c; v[1] = a - c;
+    a = v[2]; c = v[3];
+    v[2] = a + c; v[3] = a - c;
+  }
+  if (hmax > 2) {
+    float a = v[0], c = v[2];
+    v[0] = a + c; v[2] = a - c;
+    a = v[1]; c = v[3];
+    v[1] = a + c; v[3] = a - c;
+  }
+#pragma unroll
+  for (int sft = 0; sft < 6; ++sft) {
+    if ((4 << sft) >= hmax) break;
+    const bool upper = (lane >> sft) & 1;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float p = __shfl_xor(v[e], 1 << sft, 64);
+      v[e] = upper ? p - v[e] : v[e] + p;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = v[e] / L.hdiv;
+}
+
+template <bool ROT>
+__device__ void stage_z_prefetched(const LinearDesc& L, int gu0, int batch, uint16_t* zl,
+                                   int wave, int lane, const ZPrefetch& zp) {
+  const int ci = wave / batch, b = wave - ci * batch;
+  uint2 w;
+  if constexpr (ROT) {
+    float v[4], xv[4], rv[4];
+    unpack4h(zp.x0, xv);
+    unpack4h(zp.r0, rv);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = xv[e] * rv[e];
+    if (L.hb > kChunkCols) {  // hb == 512: row block o of H_2 (x) H_256
+      const int o = (((gu0 + ci) * kChunkCols) % L.hb) / kChunkCols;
+      unpack4h(zp.x1, xv);
+      unpack4h(zp.r1, rv);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += o ? -(xv[e] * rv[e]) : xv[e] * rv[e];
+    }
+    chunk_fwht(L, lane, v);
+    w.x = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
+    w.y = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
+  } else {
+    w = zp.x0;
+  }
+  *reinterpret_cast<uint2*>(zl + zl_index(b, ci * kChunkCols + lane * 4)) = w;
+}
+
+template <bool ROT>
+__device__ void stage_z(const LinearDesc& L, int gu0, int ngu, int batch, uint16_t* zl,
+                        int wave, int lane) {
+  const int items = ngu * batch;
+  for (int it = wave; it < items; it += kWavesPerGroup) {
+    const int ci = it / batch;
+    const int b = it - ci * batch;
+    const int cs = (gu0 + ci) * kChunkCols;
+    uint2 w;
+    if constexpr (ROT) {
+      float v[4];
+      rotate_chunk(L, b, cs, lane, v);
+      w.x = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
+      w.y = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
+    } else {
+      w = *reinterpret_cast<const uint2*>(L.x + (size_t)b * L.ldx + cs + lane * 4);
+    }
+    *reinterpret_cast<uint2*>(zl + zl_index(b, ci * kChunkCols + lane * 4)) = w;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host-side geometry
+// ---------------------------------------------------------------------------
+struct Geom {
+  int64_t T, G, G4, path_words, member_words;
+};
+
+inline int tiled_geom(int64_t n, int64_t d, int bits, Geom* g) {
+  if (n <= 0 || d <= 0) return TP_ERR_BAD_DIMS;
+  if (bits < 2 || bits > 4) return TP_ERR_UNSUPPORTED_BITS;
+  g->T = (n + kTileRows - 1) / kTileRows;
+  g->G4 = (d + 4 * kSegCols - 1) / (4 * kSegCols);
+  g->G = 4 * g->G4;
+  g->path_words = g->T * g->G * kTileRows * 2;
+  g->member_words = g->T * g->G * kTileRows * member_words(bits);
+  if (g->T > (1 << 26) || g->G > (1 << 20)) return TP_ERR_BAD_DIMS;
+  return TP_OK;
+}
+
+inline int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+
+// One unit (16 rows x 4 segments) of one wave: halo exchange, decode of the
+// lane's 64 weights into MFMA A operands, B operands from the staged z (lc =
+// column of this lane's segment inside the staged chunk), 8 MFMAs per batch
+// tile into acc.
+template <int KB, int NS, int NBT>
+__device__ __forceinline__ void process_unit(const uint2 X, const uint32_t* Mw, const uint32_t x1_last,
+                                             const int gu, const int lc, const int q, const int r,
+                                             const int lane, const uint32_t laneoff,
+                                             const uint32_t* table, const uint16_t* zl,
+                                             const int batch, float4_t* acc) {
+  // Halo: X1 of the previous segment, from the lane 16 below (K block q-1),
+  // or for q == 0 from the last K block's previous unit; zero at a row start.
+  const uint32_t provide = (q == 3) ? (gu == 0 ? 0u : x1_last) : X.y;
+  const uint32_t halo = (uint32_t)__shfl((int)provide, (lane + 48) & 63, 64);
+  const uint32_t P = ((halo >> 1) & 0x55555555u) | ((X.y << 1) & 0xAAAAAAAAu);
+  MemberWords<KB> m[2];
+  if constexpr (KB == 3) {
+    m[0].a = Mw[0]; m[0].b = Mw[1]; m[1].a = Mw[2]; m[1].b = Mw[3];
+  } else {
+    m[0].w = Mw[0]; m[1].w = Mw[1];
+  }
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    // B operands of this interleaved word's 4 MFMAs (batch column r).
+    half8_t zb[NBT][4];
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) {
+      const int nb = bt * 16 + r;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int off = 16 * x + (j & 2 ? 32 : 0) + (j & 1 ? 8 : 0);
+        if (nb < batch)
+          zb[bt][j] = *reinterpret_cast<const half8_t*>(zl + zl_index(nb, lc + off));
+        else
+          zb[bt][j] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    }
+    u32x4_t A[4];
+    decode_word<KB, NS>(x ? X.y : X.x, x ? X.x : P, m[x], table, laneoff, A);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const half8_t av = __builtin_bit_cast(half8_t, A[j]);
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt)
+        acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, zb[bt][j], acc[bt], 0, 0, 0);
+    }
+  }
+}
+
+}  // namespace tp

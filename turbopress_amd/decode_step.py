@@ -1,0 +1,118 @@
+"""Decode-step executors for stacks of packed linears.
+
+The reference's decode step is an HF decoder replayed from a CUDA graph with
+two Triton launches per projection (turbopress/runtime.py:312-316,
+scripts/graph_decode_bench.py:70-118).  Two MI355X executors:
+
+  * ``LinearStack`` -- every linear of the step in ONE persistent HIP launch
+    (``tp_stack_run``); optional phase ordering makes a linear of phase p
+    wait for all linears of phase p-1 (for a decoder layer: q/k/v, then o,
+    then gate/up, then down), as data dependencies would.
+  * ``layer_forward`` -- one fused launch per group of linears sharing an
+    input (q/k/v together, o, gate/up together, down): the launch structure a
+    model with interleaved attention/norm kernels uses.
+
+Inputs are fixed device buffers (write new activations into ``inputs[i]``
+before each run), outputs are fixed buffers ``outputs[i]``, so runs can be
+captured in a HIP graph and replayed.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+from torch import Tensor
+
+from turbopress_amd import _lib
+from turbopress_amd import hip_kernel as hk
+
+__all__ = ["LinearStack", "layer_forward", "QWEN_PHASES"]
+
+# Phase of each projection inside one decoder layer (shared-input groups).
+QWEN_PHASES = {"q_proj": 0, "k_proj": 0, "v_proj": 0, "o_proj": 1,
+               "gate_proj": 2, "up_proj": 2, "down_proj": 3}
+
+
+class LinearStack:
+    """A list of (PackedTCQLinear, input buffer, phase) run by one launch."""
+
+    def __init__(self, entries, ordered: bool = False) -> None:
+        if not entries:
+            raise ValueError("empty stack")
+        lins = [e[0] for e in entries]
+        l0 = lins[0]
+        for lin in lins:
+            if lin.tiled_packed is None:
+                raise ValueError("stack linears need mode='hip' with bits in (2, 3)")
+            if (lin.bits, lin.n_states) != (l0.bits, l0.n_states) or not torch.equal(lin.codebook, l0.codebook):
+                raise ValueError("stack linears must share bits, n_states and codebook")
+        self.linears = lins
+        self.inputs = [e[1] for e in entries]
+        self.phases = [int(e[2]) for e in entries]
+        if any(b < a for a, b in zip(self.phases, self.phases[1:])):
+            raise ValueError("phases must be non-decreasing along the stack")
+        self.batch = int(self.inputs[0].shape[0])
+        if not 1 <= self.batch <= 32:
+            raise ValueError("stack batch must be in [1, 32]")
+        dev = self.inputs[0].device
+        self.ordered = bool(ordered)
+        self.outputs = [torch.empty(self.batch, lin.out_features, dtype=torch.float16, device=dev)
+                        for lin in lins]
+        arr = (_lib.StackLinear * len(lins))()
+        for i, (lin, x, ph) in enumerate(zip(lins, self.inputs, self.phases)):
+            if x.dtype != torch.float16 or not x.is_contiguous() or x.shape != (self.batch, lin.in_features):
+                raise ValueError(f"input {i} must be contiguous fp16 [{self.batch}, {lin.in_features}]")
+            pb = lin._tiled_geo["path_bytes"]
+            arr[i] = _lib.StackLinear(
+                lin.tiled_packed.data_ptr(), lin.tiled_packed.data_ptr() + pb,
+                x.data_ptr(), lin.in_features, lin.rot_scale.data_ptr(), lin.block,
+                lin.scales.data_ptr(), 0 if lin.bias is None else lin.bias.data_ptr(),
+                self.outputs[i].data_ptr(), lin.out_features, lin.out_features, lin.in_features, ph, 0)
+        self.n_phases = max(self.phases) + 1
+        lib = _lib.lib()
+        nbytes = int(lib.tp_stack_plan_bytes(len(lins), self.n_phases))
+        if nbytes <= 0:
+            raise ValueError("invalid stack size")
+        self.plan = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        torch.cuda.synchronize(dev)
+        _lib.check(lib.tp_stack_plan_init(arr, len(lins), l0.bits, self.batch, self.plan.data_ptr(),
+                                          nbytes), "stack_plan_init")
+        ns = (ctypes.c_int64 * len(lins))(*[lin.out_features for lin in lins])
+        self.total_blocks = int(lib.tp_stack_plan_blocks(ns, len(lins)))
+        self.codebook = l0.codebook
+        self.bits, self.n_states = l0.bits, l0.n_states
+        self._entries = arr  # keep the host array alive with the plan
+
+    def run(self) -> list:
+        """Launch the stack on the current stream; returns the output buffers."""
+        st = _lib.lib().tp_stack_run(self.plan.data_ptr(), self.batch, self.codebook.data_ptr(),
+                                     self.bits, self.n_states, int(self.ordered), self.total_blocks,
+                                     hk.current_stream_ptr(self.plan.device))
+        _lib.check(st, "stack_run")
+        return self.outputs
+
+    def error(self) -> int:
+        """1 when a phase wait timed out in any run so far (blocking query)."""
+        out = ctypes.c_int()
+        _lib.check(_lib.lib().tp_stack_error(self.plan.data_ptr(), ctypes.byref(out)), "stack_error")
+        return int(out.value)
+
+    def algorithmic_bytes(self) -> int:
+        b = self.batch
+        return sum(l.out_features * l.in_features * l.bits // 8 + 2 * l.out_features
+                   + 2 * (1 << (l.bits + 1)) + 2 * l.in_features + 2 * b * l.in_features
+                   + 2 * b * l.out_features for l in self.linears)
+
+
+def layer_forward(mods: dict, xs: dict) -> dict:
+    """One decoder layer's projections with one launch per shared-input group:
+    q/k/v (input xs["attn"]), o (xs["o"]), gate/up (xs["mlp"]), down (xs["down"])."""
+    out = {}
+    q, k, v = hk.forward_group([mods["q_proj"], mods["k_proj"], mods["v_proj"]], xs["attn"])
+    out.update(q_proj=q, k_proj=k, v_proj=v)
+    out["o_proj"] = hk.forward_tiled(mods["o_proj"], xs["o"])
+    g, u = hk.forward_group([mods["gate_proj"], mods["up_proj"]], xs["mlp"])
+    out.update(gate_proj=g, up_proj=u)
+    out["down_proj"] = hk.forward_tiled(mods["down_proj"], xs["down"])
+    return out
