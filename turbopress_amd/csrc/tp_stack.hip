@@ -23,86 +23,131 @@ namespace tp {
 
 constexpr int kStackMaxPhases = 4096;
 
-struct StackHeader {
+// Plan layout (device memory):
+//   [0, 64)            StackCounters  -- written by the kernel (atomics)
+//   [64, ...)          StackInfo, LinearDesc[n_lin], prefix[n_lin+1],
+//                      lphase[n_lin], pblocks[n_phases]  -- read-only
+//   [pdone offset, ..) pdone[n_phases] -- written by the kernel (atomics)
+// The read-only part is passed as a separate const __restrict__ argument so
+// its loads go through the scalar cache into SGPRs.
+struct StackCounters {
   uint32_t ticket;   // next block index (reset to 0 by the last workgroup out)
   uint32_t exited;   // workgroups past the loop (reset likewise)
   uint32_t error;    // 1: a phase wait timed out; 2: launched for fewer batch rows than the plan
+  uint32_t reserved[13];
+};
+
+struct StackInfo {
   int32_t n_lin;
   int32_t total_blocks;
   int32_t n_phases;
   int32_t batch;
-  int32_t reserved;
+  int64_t pdone_offset;   // byte offset of pdone from the plan start
+  int64_t reserved;
 };
 
-struct StackPlan {  // views into the device plan buffer
-  StackHeader* h;
+struct StackRO {  // views into the read-only part
+  const StackInfo* info;
   const LinearDesc* lin;
-  const int32_t* prefix;       // [n_lin + 1] first block of each linear
-  const int32_t* lphase;       // [n_lin]
-  uint32_t* pdone;             // [n_phases] finished blocks per phase
-  const int32_t* pblocks;      // [n_phases] blocks per phase
+  const int32_t* prefix;   // [n_lin + 1] first block of each linear
+  const int32_t* lphase;   // [n_lin]
+  const int32_t* pblocks;  // [n_phases] blocks per phase
 };
+
+constexpr size_t kStackRO = sizeof(StackCounters);
 
 __host__ __device__ inline size_t stack_plan_offsets(int n_lin, int n_phases, size_t* o_lin, size_t* o_prefix,
-                                                     size_t* o_lphase, size_t* o_pdone, size_t* o_pblocks) {
-  size_t o = sizeof(StackHeader);
+                                                     size_t* o_lphase, size_t* o_pblocks, size_t* o_pdone) {
+  size_t o = kStackRO + sizeof(StackInfo);
   *o_lin = o;
   o += sizeof(LinearDesc) * (size_t)n_lin;
   *o_prefix = o;
   o += sizeof(int32_t) * (size_t)(n_lin + 1);
   *o_lphase = o;
   o += sizeof(int32_t) * (size_t)n_lin;
-  o = (o + 15) & ~(size_t)15;
-  *o_pdone = o;
-  o += sizeof(uint32_t) * (size_t)n_phases;
   *o_pblocks = o;
   o += sizeof(int32_t) * (size_t)n_phases;
+  o = (o + 63) & ~(size_t)63;
+  *o_pdone = o;
+  o += sizeof(uint32_t) * (size_t)n_phases;
   return (o + 255) & ~(size_t)255;
 }
 
-__device__ inline StackPlan stack_view(char* base, int n_lin, int n_phases) {
+// `ro` points at plan + kStackRO.
+__device__ inline StackRO stack_ro(const char* __restrict__ ro) {
+  const StackInfo* info = reinterpret_cast<const StackInfo*>(ro);
   size_t a, b, c, d, e;
-  stack_plan_offsets(n_lin, n_phases, &a, &b, &c, &d, &e);
-  StackPlan p;
-  p.h = reinterpret_cast<StackHeader*>(base);
-  p.lin = reinterpret_cast<const LinearDesc*>(base + a);
-  p.prefix = reinterpret_cast<const int32_t*>(base + b);
-  p.lphase = reinterpret_cast<const int32_t*>(base + c);
-  p.pdone = reinterpret_cast<uint32_t*>(base + d);
-  p.pblocks = reinterpret_cast<const int32_t*>(base + e);
-  return p;
+  stack_plan_offsets(info->n_lin, info->n_phases, &a, &b, &c, &d, &e);
+  StackRO v;
+  v.info = info;
+  v.lin = reinterpret_cast<const LinearDesc*>(ro + (a - kStackRO));
+  v.prefix = reinterpret_cast<const int32_t*>(ro + (b - kStackRO));
+  v.lphase = reinterpret_cast<const int32_t*>(ro + (c - kStackRO));
+  v.pblocks = reinterpret_cast<const int32_t*>(ro + (d - kStackRO));
+  return v;
+}
+
+// Path/member words of one chunk (kMaxUnitsPerBlock units) of one lane.
+template <int MW>
+struct ChunkRegs {
+  uint2 X[kMaxUnitsPerBlock];
+  uint32_t M[kMaxUnitsPerBlock][MW];
+};
+
+template <int MW>
+__device__ __forceinline__ ChunkRegs<MW> load_chunk(const LinearDesc& L, const uint32_t* pt, const uint32_t* mt,
+                                                     int ch, bool active, int q, int r) {
+  // Branch-free: units past the block's K range (and inactive waves, whose
+  // pointers address tile 0) reload unit 0 of the chunk; they are never used.
+  ChunkRegs<MW> c;
+  const int gu0 = ch * kMaxUnitsPerBlock;
+  const int ngu = min(kMaxUnitsPerBlock, L.G4 - gu0);
+  (void)active;
+#pragma unroll
+  for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
+    const int g = 4 * (gu0 + (u < ngu ? u : 0)) + q;
+    c.X[u] = gld2(pt + (g * kTileRows + r) * 2);
+#pragma unroll
+    for (int i = 0; i < MW; ++i) c.M[u][i] = gld(mt + (g * kTileRows + r) * MW + i);
+  }
+  return c;
 }
 
 template <int KB, int NS, int NBT>
 __global__ void __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(NBT == 1 ? 4 : 2)))
-tcq_stack_kernel(char* plan_base, const uint16_t* codebook, int ordered, int spin_limit) {
+tcq_stack_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
+                 const uint16_t* __restrict__ codebook, int ordered, int spin_limit, int zrows) {
   __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
   extern __shared__ __attribute__((aligned(16))) uint16_t zl[];
   __shared__ int s_next;
   constexpr int MW = member_words(KB);
   // Sizes come from the plan itself, never from the caller.
-  const StackHeader* H0 = reinterpret_cast<const StackHeader*>(plan_base);
-  const int n_lin = H0->n_lin;
-  const int n_phases = H0->n_phases;
-  const int batch = H0->batch;
-  const StackPlan P = stack_view(plan_base, n_lin, n_phases);
-  if (batch > 16 * NBT) {  // staged z rows would not fit: refuse uniformly
-    if (threadIdx.x == 0 && blockIdx.x == 0) atomicExch(&P.h->error, 2u);
+  const StackRO P = stack_ro(plan_ro);
+  const int n_lin = P.info->n_lin;
+  const int n_phases = P.info->n_phases;
+  const int batch = P.info->batch;
+  const int total = P.info->total_blocks;
+  StackCounters* C = reinterpret_cast<StackCounters*>(plan_rw);
+  uint32_t* pdone = reinterpret_cast<uint32_t*>(plan_rw + P.info->pdone_offset);
+  if (batch > 16 * NBT || batch > zrows) {  // staged z rows would not fit: refuse uniformly
+    if (threadIdx.x == 0 && blockIdx.x == 0) atomicExch(&C->error, 2u);
     return;
   }
-  const int total = P.h->total_blocks;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int r = lane & 15;
   const int q = lane >> 4;
   const uint32_t laneoff = (uint32_t)lane << 2;
-  const uint32_t cb_lane = codebook[lane & ((2 << KB) - 1)];
+  const uint32_t cb_lane = gld(codebook + (lane & ((2 << KB) - 1)));
 
-  if (tid == 0) s_next = (int)atomicAdd(&P.h->ticket, 1u);
+  if (tid == 0) s_next = (int)atomicAdd(&C->ticket, 1u);
   build_pair_table_lanes<KB>(table, cb_lane, tid, kGroupThreads);
   __syncthreads();
-  int blk = s_next;
+  // The ticket travels through LDS; make its uniformity explicit so that the
+  // descriptor reads below become scalar loads (vector loads would be followed
+  // by waits that also drain the weight prefetches in flight).
+  int blk = __builtin_amdgcn_readfirstlane(s_next);
 
   while (blk < total) {
     // Linear of this block: last li with prefix[li] <= blk (uniform).
@@ -111,8 +156,8 @@ tcq_stack_kernel(char* plan_base, const uint16_t* codebook, int ordered, int spi
       const int mid = (lo + hi + 1) >> 1;
       if (P.prefix[mid] <= blk) lo = mid; else hi = mid - 1;
     }
-    const int li = lo;
-    const LinearDesc& L = P.lin[li];
+    const int li = __builtin_amdgcn_readfirstlane(lo);
+    const LinearDesc L = P.lin[li];  // copied to registers once per block
     const int t = (blk - P.prefix[li]) * kWavesPerGroup + wave;
     const bool active = t < L.T;
     const int nch = (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock;
@@ -121,7 +166,7 @@ tcq_stack_kernel(char* plan_base, const uint16_t* codebook, int ordered, int spi
 
     // Claim the next block now; its index is needed only after this one.
     uint32_t next_ticket = 0;
-    if (tid == 0) next_ticket = atomicAdd(&P.h->ticket, 1u);
+    if (tid == 0) next_ticket = atomicAdd(&C->ticket, 1u);
 
     if (ordered) {
       const int ph = P.lphase[li];
@@ -129,9 +174,9 @@ tcq_stack_kernel(char* plan_base, const uint16_t* codebook, int ordered, int spi
         if (tid == 0) {
           const uint32_t need = (uint32_t)P.pblocks[ph - 1];
           int spins = 0;
-          while (__hip_atomic_load(&P.pdone[ph - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+          while (__hip_atomic_load(&pdone[ph - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
             if (++spins > spin_limit) {
-              atomicExch(&P.h->error, 1u);
+              atomicExch(&C->error, 1u);
               break;
             }
             __builtin_amdgcn_s_sleep(8);
@@ -141,51 +186,20 @@ tcq_stack_kernel(char* plan_base, const uint16_t* codebook, int ordered, int spi
       }
     }
 
-    // Loads of chunk 0.
+    // Chunks run ping-pong over two register sets (A, B): a set is refilled
+    // only after its last use, so the prefetched values never need a register
+    // copy (a copy would have to wait for the prefetch to land).
     uint32_t x1_last = 0;
-    uint2 X[kMaxUnitsPerBlock];
-    uint32_t Mw[kMaxUnitsPerBlock][MW];
-    auto load_chunk = [&](int ch, uint2* Xo, uint32_t (*Mo)[MW]) {
-      const int gu0 = ch * kMaxUnitsPerBlock;
-      const int ngu = min(kMaxUnitsPerBlock, L.G4 - gu0);
-#pragma unroll
-      for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
-        Xo[u] = uint2{0u, 0u};
-#pragma unroll
-        for (int i = 0; i < MW; ++i) Mo[u][i] = 0;
-        if (active && u < ngu) {
-          const int g = 4 * (gu0 + u) + q;
-          Xo[u] = *reinterpret_cast<const uint2*>(pt + (g * kTileRows + r) * 2);
-#pragma unroll
-          for (int i = 0; i < MW; ++i) Mo[u][i] = mt[(g * kTileRows + r) * MW + i];
-        }
-      }
-    };
-    load_chunk(0, X, Mw);
-    ZPrefetch zp;
-    prefetch_z<true>(L, 0, min(kMaxUnitsPerBlock, L.G4), batch, wave, lane, zp);
-
     float4_t acc[NBT];
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
-
-    for (int ch = 0; ch < nch; ++ch) {
+    auto chunk_body = [&](int ch, const ChunkRegs<MW>& regs, const ZPrefetch& zpf) {
       const int gu0 = ch * kMaxUnitsPerBlock;
       const int ngu = min(kMaxUnitsPerBlock, L.G4 - gu0);
-      // Loads of the next chunk go out before this chunk's LDS work.
-      uint2 Xn[kMaxUnitsPerBlock];
-      uint32_t Mn[kMaxUnitsPerBlock][MW];
-      ZPrefetch zpn;
-      zpn.valid = false;
-      if (ch + 1 < nch) {
-        load_chunk(ch + 1, Xn, Mn);
-        prefetch_z<true>(L, gu0 + kMaxUnitsPerBlock, min(kMaxUnitsPerBlock, L.G4 - gu0 - kMaxUnitsPerBlock),
-                         batch, wave, lane, zpn);
-      }
       const bool small = ngu * batch <= kWavesPerGroup && L.hb <= 2 * kChunkCols;
       __syncthreads();  // z of the previous chunk is no longer read
       if (small) {
-        if (zp.valid) stage_z_prefetched<true>(L, gu0, batch, zl, wave, lane, zp);
+        if (zpf.valid) stage_z_prefetched<true>(L, gu0, batch, zl, wave, lane, zpf);
       } else {
         stage_z<true>(L, gu0, ngu, batch, zl, wave, lane);
       }
@@ -195,20 +209,23 @@ tcq_stack_kernel(char* plan_base, const uint16_t* codebook, int ordered, int spi
         for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
           if (u >= ngu) break;
           const int gu = gu0 + u;
-          process_unit<KB, NS, NBT>(X[u], Mw[u], x1_last, gu, (4 * gu + q - 4 * gu0) * kSegCols, q, r,
+          process_unit<KB, NS, NBT>(regs.X[u], regs.M[u], x1_last, gu, (4 * gu + q - 4 * gu0) * kSegCols, q, r,
                                     lane, laneoff, table, zl, batch, acc);
-          x1_last = X[u].y;
+          x1_last = regs.X[u].y;
         }
       }
-      if (ch + 1 < nch) {
-#pragma unroll
-        for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
-          X[u] = Xn[u];
-#pragma unroll
-          for (int i = 0; i < MW; ++i) Mw[u][i] = Mn[u][i];
-        }
-        zp = zpn;
-      }
+    };
+    auto ngu_of = [&](int ch) { return ch < nch ? min(kMaxUnitsPerBlock, L.G4 - ch * kMaxUnitsPerBlock) : 0; };
+    ChunkRegs<MW> ra = load_chunk<MW>(L, pt, mt, 0, active, q, r);
+    ZPrefetch za = prefetch_z<true>(L, 0, ngu_of(0), batch, wave, lane);
+    for (int ch = 0; ch < nch; ch += 2) {
+      const ChunkRegs<MW> rb = load_chunk<MW>(L, pt, mt, ch + 1 < nch ? ch + 1 : ch, active && ch + 1 < nch, q, r);
+      const ZPrefetch zb = prefetch_z<true>(L, (ch + 1) * kMaxUnitsPerBlock, ngu_of(ch + 1), batch, wave, lane);
+      chunk_body(ch, ra, za);
+      if (ch + 1 >= nch) break;
+      ra = load_chunk<MW>(L, pt, mt, ch + 2 < nch ? ch + 2 : ch, active && ch + 2 < nch, q, r);
+      za = prefetch_z<true>(L, (ch + 2) * kMaxUnitsPerBlock, ngu_of(ch + 2), batch, wave, lane);
+      chunk_body(ch + 1, rb, zb);
     }
 
     // Full-K epilogue: lane holds rows 4q..4q+3 of its tile for batch column r.
@@ -218,43 +235,49 @@ tcq_stack_kernel(char* plan_base, const uint16_t* codebook, int ordered, int spi
       for (int i = 0; i < 4; ++i) {
         const int row = row0 + i;
         if (row >= L.n) continue;
-        const float sc = h2f(L.scales[row]);
-        const float bs = L.bias ? h2f(L.bias[row]) : 0.f;
+        const float sc = h2f(gld(L.scales + row));
+        const float bs = L.bias ? h2f(gld(L.bias + row)) : 0.f;
 #pragma unroll
         for (int bt = 0; bt < NBT; ++bt) {
           const int nb = bt * 16 + r;
           if (nb >= batch) continue;
           uint16_t out = f2h(acc[bt][i] * sc);
           if (L.bias) out = f2h(h2f(out) + bs);
-          L.y[(size_t)nb * L.ldy + row] = out;
+          gst(L.y + (size_t)nb * L.ldy + row, out);
         }
       }
     }
     if (ordered) {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      if (tid == 0) atomicAdd(&P.pdone[P.lphase[li]], 1u);
+      if (tid == 0) atomicAdd(&pdone[P.lphase[li]], 1u);
     }
     if (tid == 0) s_next = (int)next_ticket;
     __syncthreads();
-    blk = s_next;
+    blk = __builtin_amdgcn_readfirstlane(s_next);
   }
 
   // The last workgroup out resets the counters for the next launch.
   if (tid == 0) {
-    const uint32_t e = atomicAdd(&P.h->exited, 1u);
+    const uint32_t e = atomicAdd(&C->exited, 1u);
     if (e == gridDim.x - 1) {
-      for (int p = 0; p < n_phases; ++p) atomicExch(&P.pdone[p], 0u);
-      atomicExch(&P.h->ticket, 0u);
-      atomicExch(&P.h->exited, 0u);
+      for (int p = 0; p < n_phases; ++p) atomicExch(&pdone[p], 0u);
+      atomicExch(&C->ticket, 0u);
+      atomicExch(&C->exited, 0u);
     }
   }
 }
 
+// z staging rows: 8 for batch <= 8 keeps table + z + ticket slot within half
+// of the 160 KiB LDS, so two workgroups share a CU.
+inline int stack_z_rows(int64_t batch) { return batch <= 8 ? 8 : batch <= 16 ? 16 : 32; }
+
 template <int KB, int NS, int NBT>
-void launch_stack(char* plan, int grid, const uint16_t* cb, int ordered, int spin_limit, hipStream_t s) {
+void launch_stack(char* plan, int grid, int64_t batch, const uint16_t* cb, int ordered, int spin_limit,
+                  hipStream_t s) {
   hipLaunchKernelGGL((tcq_stack_kernel<KB, NS, NBT>), dim3(grid), dim3(kGroupThreads),
-                     (size_t)16 * NBT * kZCols * 2, s, plan, cb, ordered, spin_limit);
+                     (size_t)stack_z_rows(batch) * kZCols * 2, s, (const char*)(plan + kStackRO), plan, cb,
+                     ordered, spin_limit, stack_z_rows(batch));
 }
 
 }  // namespace tp
@@ -279,12 +302,12 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     if (linears[i].phase + 1 > n_phases) n_phases = linears[i].phase + 1;
   }
   size_t o_lin, o_prefix, o_lphase, o_pdone, o_pblocks;
-  const size_t need = stack_plan_offsets(n_linears, n_phases, &o_lin, &o_prefix, &o_lphase, &o_pdone, &o_pblocks);
+  const size_t need = stack_plan_offsets(n_linears, n_phases, &o_lin, &o_prefix, &o_lphase, &o_pblocks, &o_pdone);
   if (plan_bytes < (int64_t)need) return TP_ERR_WORKSPACE;
   if ((uintptr_t)plan & 255) return TP_ERR_MISALIGNED;
   char* host = (char*)calloc(1, need);
   if (!host) return TP_ERR_HIP;
-  StackHeader* h = reinterpret_cast<StackHeader*>(host);
+  StackInfo* h = reinterpret_cast<StackInfo*>(host + kStackRO);
   LinearDesc* lin = reinterpret_cast<LinearDesc*>(host + o_lin);
   int32_t* prefix = reinterpret_cast<int32_t*>(host + o_prefix);
   int32_t* lphase = reinterpret_cast<int32_t*>(host + o_lphase);
@@ -341,6 +364,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     h->total_blocks = (int32_t)total;
     h->n_phases = n_phases;
     h->batch = (int32_t)batch;
+    h->pdone_offset = (int64_t)o_pdone;
     if (hipMemcpy(plan, host, need, hipMemcpyHostToDevice) != hipSuccess) st = TP_ERR_HIP;
   }
   free(host);
@@ -354,14 +378,14 @@ extern "C" int tp_stack_run(void* plan, int64_t batch, const uint16_t* codebook,
   if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
   const int nbt = batch <= 16 ? 1 : 2;
   const int cus = device_cu_count();
-  const int per_cu = nbt == 1 ? 2 : 1;
+  const int per_cu = batch <= 8 ? 2 : 1;
   const int grid = (int)(total_blocks < (int64_t)cus * per_cu ? total_blocks : (int64_t)cus * per_cu);
   const int spin_limit = 1 << 22;  // ~ seconds of s_sleep polling; ends the wait regardless
   char* p = reinterpret_cast<char*>(plan);
   hipStream_t s = (hipStream_t)stream;
 #define TP_STACK(KB, NS)                                                       \
-  (nbt == 1 ? launch_stack<KB, NS, 1>(p, grid, codebook, ordered, spin_limit, s) \
-            : launch_stack<KB, NS, 2>(p, grid, codebook, ordered, spin_limit, s))
+  (nbt == 1 ? launch_stack<KB, NS, 1>(p, grid, batch, codebook, ordered, spin_limit, s) \
+            : launch_stack<KB, NS, 2>(p, grid, batch, codebook, ordered, spin_limit, s))
   switch (bits * 100 + n_states) {
     case 204: TP_STACK(2, 4); break;
     case 208: TP_STACK(2, 8); break;
@@ -390,7 +414,7 @@ extern "C" int64_t tp_stack_plan_blocks(const int64_t* ns, int n_linears) {
 
 extern "C" int tp_stack_error(const void* plan, int* error_out) {
   if (!plan || !error_out) return TP_ERR_NULL_POINTER;
-  StackHeader h;
+  StackCounters h;
   if (hipMemcpy(&h, plan, sizeof(h), hipMemcpyDeviceToHost) != hipSuccess) return TP_ERR_HIP;
   *error_out = (int)h.error;
   return TP_OK;

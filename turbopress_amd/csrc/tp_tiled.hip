@@ -108,8 +108,7 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
         }
       }
     }
-    ZPrefetch zp;
-    prefetch_z<ROT>(L, gu0, ngu, batch, wave, lane, zp);
+    const ZPrefetch zp = prefetch_z<ROT>(L, gu0, ngu, batch, wave, lane);
     const bool small = ngu * batch <= kWavesPerGroup && (!ROT || L.hb <= 2 * kChunkCols);
 
     __syncthreads();  // every wave is done reading the previous block's z

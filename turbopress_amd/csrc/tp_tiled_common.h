@@ -10,6 +10,25 @@
 namespace tp {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+
+// Loads/stores through the global address space.  Pointers read from a
+// device-side descriptor table are generic to the compiler; generic (flat)
+// accesses count against both the vector-memory and the LDS wait counters,
+// so an LDS wait would also drain every prefetch in flight.
+#define TP_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ T gld(const T* p) {
+  return *(const TP_GLOBAL T*)p;
+}
+template <typename T>
+__device__ __forceinline__ void gst(T* p, T v) {
+  *(TP_GLOBAL T*)p = v;
+}
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint2 gld2(const void* p) {
+  const u32x2_t v = *(const TP_GLOBAL u32x2_t*)p;
+  return uint2{v.x, v.y};
+}
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -193,7 +212,7 @@ __device__ __forceinline__ int zl_index(int row, int col) {
 }
 
 __device__ __forceinline__ void load4h(const uint16_t* p, float v[4]) {
-  const uint2 w = *reinterpret_cast<const uint2*>(p);
+  const uint2 w = gld2((p));
   v[0] = h2f((uint16_t)w.x);
   v[1] = h2f((uint16_t)(w.x >> 16));
   v[2] = h2f((uint16_t)w.y);
@@ -219,7 +238,7 @@ __device__ void rotate_chunk(const LinearDesc& L, int b, int cs, int lane, float
     } else {
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        if (c0 + e < L.d) v[e] = h2f(xr[c0 + e]) * h2f(L.rs[c0 + e]);
+        if (c0 + e < L.d) v[e] = h2f(gld(xr + c0 + e)) * h2f(gld(L.rs + c0 + e));
     }
   } else {
     const int base = cs - cs % hb;
@@ -266,38 +285,40 @@ __device__ void rotate_chunk(const LinearDesc& L, int b, int cs, int lane, float
 // common small case (at most one item per wave, Hadamard block <= 512) keeps
 // every load of the block in flight before the first barrier.
 struct ZPrefetch {
-  bool valid;
+  bool valid;   // this wave stages an item of the chunk
+  bool inb;     // the lane's 4 columns lie inside d (else they read as zero)
   uint2 x0, r0, x1, r1;
 };
 
+// Branch-free: every wave always issues its four loads from clamped, valid
+// addresses (loads issued under divergent control flow would have to be
+// waited for where their registers merge), and validity travels as flags.
 template <bool ROT>
-__device__ __forceinline__ void prefetch_z(const LinearDesc& L, int gu0, int ngu, int batch,
-                                           int wave, int lane, ZPrefetch& zp) {
-  zp.valid = false;
+__device__ __forceinline__ ZPrefetch prefetch_z(const LinearDesc& L, int gu0, int ngu, int batch,
+                                                int wave, int lane) {
+  ZPrefetch zp;
   const int items = ngu * batch;
-  if (items > kWavesPerGroup || wave >= items || (ROT && L.hb > 2 * kChunkCols)) return;
-  const int ci = wave / batch, b = wave - ci * batch;
+  zp.valid = !(items > kWavesPerGroup || wave >= items || (ROT && L.hb > 2 * kChunkCols));
+  const int it = zp.valid ? wave : 0;
+  const int ci = it / batch, b = it - ci * batch;
   const int cs = (gu0 + ci) * kChunkCols;
-  zp.valid = true;
-  zp.x0 = zp.r0 = zp.x1 = zp.r1 = uint2{0u, 0u};
   if constexpr (ROT) {
     const uint16_t* xr = L.x + (size_t)b * L.ldx;
-    if (L.hb <= kChunkCols) {
-      const int c0 = cs + lane * 4;
-      if (c0 < L.d) {
-        zp.x0 = *reinterpret_cast<const uint2*>(xr + c0);
-        zp.r0 = *reinterpret_cast<const uint2*>(L.rs + c0);
-      }
-    } else {
-      const int c0 = cs - cs % L.hb + lane * 4;
-      zp.x0 = *reinterpret_cast<const uint2*>(xr + c0);
-      zp.r0 = *reinterpret_cast<const uint2*>(L.rs + c0);
-      zp.x1 = *reinterpret_cast<const uint2*>(xr + c0 + kChunkCols);
-      zp.r1 = *reinterpret_cast<const uint2*>(L.rs + c0 + kChunkCols);
-    }
+    const bool big = L.hb > kChunkCols;
+    int c0 = (big ? cs - cs % L.hb : cs) + lane * 4;
+    zp.inb = c0 < L.d;
+    c0 = zp.inb ? c0 : 0;
+    const int c1 = big ? c0 + kChunkCols : c0;
+    zp.x0 = gld2(xr + c0);
+    zp.r0 = gld2(L.rs + c0);
+    zp.x1 = gld2(xr + c1);
+    zp.r1 = gld2(L.rs + c1);
   } else {
-    zp.x0 = *reinterpret_cast<const uint2*>(L.x + (size_t)b * L.ldx + cs + lane * 4);
+    zp.inb = true;
+    zp.x0 = gld2(L.x + (size_t)b * L.ldx + cs + lane * 4);
+    zp.r0 = zp.x1 = zp.r1 = uint2{0u, 0u};
   }
+  return zp;
 }
 
 __device__ __forceinline__ void unpack4h(uint2 w, float v[4]) {
@@ -347,7 +368,7 @@ __device__ void stage_z_prefetched(const LinearDesc& L, int gu0, int batch, uint
     unpack4h(zp.x0, xv);
     unpack4h(zp.r0, rv);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] = xv[e] * rv[e];
+    for (int e = 0; e < 4; ++e) v[e] = zp.inb ? xv[e] * rv[e] : 0.f;
     if (L.hb > kChunkCols) {  // hb == 512: row block o of H_2 (x) H_256
       const int o = (((gu0 + ci) * kChunkCols) % L.hb) / kChunkCols;
       unpack4h(zp.x1, xv);
@@ -379,7 +400,7 @@ __device__ void stage_z(const LinearDesc& L, int gu0, int ngu, int batch, uint16
       w.x = (uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16);
       w.y = (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16);
     } else {
-      w = *reinterpret_cast<const uint2*>(L.x + (size_t)b * L.ldx + cs + lane * 4);
+      w = gld2((L.x + (size_t)b * L.ldx + cs + lane * 4));
     }
     *reinterpret_cast<uint2*>(zl + zl_index(b, ci * kChunkCols + lane * 4)) = w;
   }

@@ -45,7 +45,7 @@ class LinearStack:
         for lin in lins:
             if lin.tiled_packed is None:
                 raise ValueError("stack linears need mode='hip' with bits in (2, 3)")
-            if (lin.bits, lin.n_states) != (l0.bits, l0.n_states) or not torch.equal(lin.codebook, l0.codebook):
+            if (lin.bits, lin.n_states) != (l0.bits, l0.n_states) or lin.codebook_key != l0.codebook_key:
                 raise ValueError("stack linears must share bits, n_states and codebook")
         self.linears = lins
         self.inputs = [e[1] for e in entries]

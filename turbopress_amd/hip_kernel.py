@@ -256,7 +256,7 @@ def forward_group(layers, x: Tensor) -> list:
         if lyr.tiled_packed is None or lyr.in_features != d or lyr.bits != l0.bits \
                 or lyr.n_states != l0.n_states:
             raise ValueError("grouped layers need the device layout and equal in_features/bits/S")
-        if not torch.equal(lyr.codebook, l0.codebook):
+        if lyr.codebook_key != l0.codebook_key:
             raise ValueError("grouped layers must share one codebook")
     if d % 4:
         return [forward_tiled(lyr, x) for lyr in layers]

@@ -109,6 +109,9 @@ class PackedTCQLinear(nn.Module):
         self.register_buffer("bias", buf("bias", torch.float16))
         self.register_buffer("lut", hk.subset_lut(self.n_states).to(dev))
         self._check_shapes()
+        # Host-side codebook fingerprint: grouped launches compare it without
+        # touching the device (legal while a graph is being captured).
+        self.codebook_key = tuple(self.codebook.cpu().view(torch.int16).tolist())
         # Fused activation-side scale (runtime.py:243-249): fp16((2s-1)*inv_equil),
         # formed on the GPU from the packed sign bits.
         d = self.in_features
