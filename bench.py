@@ -11,18 +11,22 @@ shared-input group (q/k/v, o, gate/up, down) of every layer.  The weights
 HBM.  A step is captured once in a HIP graph and replayed; K replays are
 timed with HIP events between two device synchronisations.
 
-``value`` (µs per step, lower is better) is the primary executor: one
-persistent launch for all 252 linears (tp_stack_run) with the decoder's data
-dependencies enforced on the device -- every linear of phase p (q/k/v | o |
-gate/up | down of each layer, 144 phases) waits for all of phase p-1.  The
-line also reports the same step without the ordering, with one launch per
-shared-input group (144 launches) and with one launch per linear (252
-launches, the drop-in PackedTCQLinear.forward path).
+``value`` (µs per step, lower is better) is the primary executor, the
+decode-step stack (tp_stack_run): one small launch rotates all 252 inputs
+(z = blockFWHT(x * rot_scale) / sqrt(block), fp16) into the plan's z buffer,
+then ONE persistent launch streams every linear's packed weights.  The line
+also reports the same stack with the decoder's phase order enforced on the
+device (q/k/v | o | gate/up | down of each layer, 144 phases, a phase starts
+after all of the previous one), one launch per shared-input group (144
+launches) and one launch per linear (252 launches, the drop-in
+PackedTCQLinear.forward path).
 
-``roofline`` covers the dominant kernel (the stack kernel: one launch per
-step moves the whole step's algorithmic bytes); ``cpu_baseline`` times the
-reference's CPU tiled path (the oracle's op-for-op restatement) on a bounded
-sample on this host.
+``roofline`` covers the dominant kernel, the stack's GEMV launch
+(tcq_stack_slot_kernel): its algorithmic bytes (the step's bytes minus the
+rot_scale vectors, which only the rotation launch reads) over its own
+duration, timed with HIP events around back-to-back launches on the stream
+they run on.  ``cpu_baseline`` times the reference's CPU tiled path (the
+oracle's op-for-op restatement) on a bounded sample on this host.
 """
 
 from __future__ import annotations
@@ -107,6 +111,25 @@ def time_graph(step_fn, steps, warmup):
     return start.elapsed_time(end) / steps, wall / steps * 1e3, g
 
 
+def time_gemv_kernel(stack, steps, warmup):
+    """Average duration (µs) of the stack's GEMV launch alone: the z buffer is
+    filled once, then `steps` GEMV launches run back to back between two
+    events on the stream they are launched on."""
+    stack.rotate()
+    for _ in range(warmup):
+        stack.gemv()
+    torch.cuda.synchronize()
+    for _ in range(warmup):  # back at the sustained clock after the host sync above
+        stack.gemv()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        stack.gemv()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps * 1e3
+
+
 def cpu_baseline(budget_s: float):
     """The reference's CPU tiled path (oracle restatement), one Qwen3-4B layer
     at k=3, B=1, repeated until ~budget_s of CPU work, scaled to 36 layers."""
@@ -142,8 +165,11 @@ def cpu_baseline(budget_s: float):
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    # The GPU's power management lowers the clock after ~1.5 ms of this
+    # load and settles within ~100 steps: the default warmup reaches that
+    # steady state before the timed steps.
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-primary", action="store_true", help="skip the comparison executors")
@@ -163,16 +189,18 @@ def main() -> int:
     nbytes = step_bytes(layers)
     log(f"{nbytes / 1e9:.4f} GB per step")
 
-    stack_o = make_stack(layers, inputs, ordered=True)
-    ms, ms_wall, _ = time_graph(stack_o.run, args.steps, args.warmup)
-    if stack_o.error():
-        raise RuntimeError("stack phase wait timed out")
-    log(f"stack (ordered, 1 launch): {ms * 1e3:.1f} us/step")
+    stack = make_stack(layers, inputs, ordered=False)
+    ms, ms_wall, _ = time_graph(stack.run, args.steps, args.warmup)
+    log(f"stack (rotation launch + 1 GEMV launch): {ms * 1e3:.1f} us/step")
+    us_gemv = time_gemv_kernel(stack, args.steps, args.warmup)
+    log(f"stack GEMV kernel alone: {us_gemv:.1f} us/launch")
     extra = {}
     if not args.only_primary:
-        stack_u = make_stack(layers, inputs, ordered=False)
-        ms_u, _, _ = time_graph(stack_u.run, args.steps, args.warmup)
-        log(f"stack (unordered, 1 launch): {ms_u * 1e3:.1f} us/step")
+        stack_o = make_stack(layers, inputs, ordered=True)
+        ms_o, _, _ = time_graph(stack_o.run, max(5, args.steps // 5), 2)
+        if stack_o.error():
+            raise RuntimeError("stack phase wait timed out")
+        log(f"stack, phase-ordered: {ms_o * 1e3:.1f} us/step")
         steps_slow = max(5, args.steps // 5)
 
         def grouped():
@@ -189,7 +217,7 @@ def main() -> int:
 
         ms_p, _, _ = time_graph(per_linear, steps_slow, 2)
         log(f"per-linear launches (252/step): {ms_p * 1e3:.1f} us/step")
-        extra = {"unordered_stack_us": round(ms_u * 1e3, 2), "grouped_launches_us": round(ms_g * 1e3, 2),
+        extra = {"phase_ordered_stack_us": round(ms_o * 1e3, 2), "grouped_launches_us": round(ms_g * 1e3, 2),
                  "per_linear_launches_us": round(ms_p * 1e3, 2)}
 
     cpu = None
@@ -197,6 +225,8 @@ def main() -> int:
         log("CPU baseline")
         cpu = cpu_baseline(args.cpu_seconds)
     gbps = nbytes / (ms * 1e-3) / 1e9
+    gemv_bytes = nbytes - sum(2 * m.in_features for mods in layers for m in mods.values())
+    gemv_gbps = gemv_bytes / (us_gemv * 1e-6) / 1e9
     line = {
         "metric": "µs per decode-step linear stack + HBM GB/s (% peak), 3-bit TCQ, Qwen3-4B b=1",
         "value": round(ms * 1e3, 2), "unit": "us/step", "n_gpus": 1,
@@ -204,15 +234,15 @@ def main() -> int:
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp16", "data": "synthetic (seeded codes, codebook, scales, signs, activations)",
         "config": {"workload": "qwen3-4b decode-step linear stack: 36 layers x (q,k,v,o,gate,up,down), "
-                               "one HIP graph, one persistent launch, phases q/k/v->o->gate/up->down "
-                               "enforced on device", "layers": N_LAYERS, "bits": BITS,
-                   "n_states": N_STATES, "batch": BATCH, "bytes_per_step": nbytes},
+                               "one HIP graph: rotation launch + one persistent GEMV launch",
+                   "layers": N_LAYERS, "bits": BITS, "n_states": N_STATES, "batch": BATCH,
+                   "bytes_per_step": nbytes},
         "gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
         "wall_ms_per_step": round(ms_wall, 5),
-        "roofline": {"kernel": "tcq_stack_kernel<3,64,1> (all 252 linears, one launch per step)",
-                     "bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "us_per_launch": round(ms * 1e3, 2), "bytes_per_launch": nbytes},
+        "roofline": {"kernel": "tcq_stack_slot_kernel<3,64,2> (all 252 linears, one launch per step)",
+                     "bound": "hbm", "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "us_per_launch": round(us_gemv, 2), "bytes_per_launch": gemv_bytes},
         "executors": extra,
         "cpu_baseline": cpu,
     }

@@ -224,9 +224,10 @@ typedef struct tp_stack_linear {
   int32_t reserved;
 } tp_stack_linear;
 
-/* Bytes of the device plan for n_linears linears in n_phases phases (0 when
- * invalid).  Host only. */
-int64_t tp_stack_plan_bytes(int n_linears, int n_phases);
+/* Bytes of the device plan of these linears at this batch (0 when invalid):
+ * descriptors, schedules, counters and, for batch <= 8, the buffer of
+ * rotated activations (batch * ceil(d/256)*256 fp16 per linear).  Host only. */
+int64_t tp_stack_plan_bytes(const tp_stack_linear* linears, int n_linears, int bits, int64_t batch);
 
 /* Validate the linears and write the plan (descriptors, block prefix sums,
  * phase tables, zeroed counters, batch in [1, 32]) into `plan` (device
@@ -237,7 +238,9 @@ int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears, int bits,
                        int64_t batch, void* plan, int64_t plan_bytes);
 
 /* Run every linear of the plan (y = PackedTCQLinear.forward(x) for each, as
- * tp_packed_linear_forward computes it) in ONE persistent launch.  With
+ * tp_packed_linear_forward computes it): for batch <= 8 one small launch
+ * rotates every input into the plan's z buffer and ONE persistent launch
+ * runs all GEMVs; for batch 9..32 one persistent launch does both.  With
  * ordered != 0 a linear of phase p starts only after all linears of phase
  * p-1 finished.  The plan's counters return to zero after each run, so one
  * plan serves any number of runs or graph replays on one stream (runs that
@@ -247,6 +250,15 @@ int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears, int bits,
  * does nothing. */
 int tp_stack_run(void* plan, int64_t batch, const uint16_t* codebook, int bits,
                  int n_states, int ordered, int64_t total_blocks, void* stream);
+
+/* The two launches of tp_stack_run, for callers that schedule them apart:
+ * tp_stack_rotate fills the plan's z buffer from the current inputs (a no-op
+ * for batch > 8); tp_stack_gemv runs the GEMVs from it (batch <= 8) or from
+ * the inputs directly (batch > 8).  A tp_stack_gemv run after new inputs
+ * were written needs a tp_stack_rotate in between on the same stream. */
+int tp_stack_rotate(void* plan, int64_t batch, void* stream);
+int tp_stack_gemv(void* plan, int64_t batch, const uint16_t* codebook, int bits,
+                  int n_states, int ordered, int64_t total_blocks, void* stream);
 
 /* Work blocks of a stack of linears with the given (n) sizes: sum of
  * ceil(ceil(n/16)/8).  Host only. */

@@ -35,8 +35,10 @@ def _check(payloads, stack):
 
 
 @pytest.mark.parametrize("ordered", [False, True])
-@pytest.mark.parametrize("batch", [1, 5, 20])
+@pytest.mark.parametrize("batch", [1, 2, 3, 5, 8, 12, 20])
 def test_stack_matches_oracle(cuda, ordered, batch):
+    """Batch 1-2 / 3-4 / 5-8: slot kernel with 8 / 4 / 2 slots per z load;
+    9-16 / 17-32: LDS-staged kernel with one / two batch tiles."""
     payloads, stack = _build(cuda, MIXED, batch, ordered=ordered, bias=True)
     stack.run()
     torch.cuda.synchronize()

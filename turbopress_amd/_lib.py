@@ -63,9 +63,11 @@ class StackLinear(ctypes.Structure):
 
 
 SIGNATURES.update({
-    "tp_stack_plan_bytes": (c_int64, [c_int, c_int]),
+    "tp_stack_plan_bytes": (c_int64, [POINTER(StackLinear), c_int, c_int, _I64]),
     "tp_stack_plan_init": (c_int, [POINTER(StackLinear), c_int, c_int, _I64, _P, _I64]),
     "tp_stack_run": (c_int, [_P, _I64, _P, c_int, c_int, c_int, _I64, _P]),
+    "tp_stack_rotate": (c_int, [_P, _I64, _P]),
+    "tp_stack_gemv": (c_int, [_P, _I64, _P, c_int, c_int, c_int, _I64, _P]),
     "tp_stack_plan_blocks": (c_int64, [POINTER(c_int64), c_int]),
     "tp_stack_error": (c_int, [_P, POINTER(c_int)]),
 })

@@ -27,9 +27,13 @@ ARCH = os.environ.get("TP_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -packed-fp32-ops: keep the compiler from emitting packed fp32 VALU ops.
+# atomic optimizer off: it turns a one-lane ticket atomicAdd into a wave
+# reduction whose result is read back at once, i.e. a wait that would drain
+# every weight prefetch in flight; the kernels consume ticket results later.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-munsafe-fp-atomics", "-Wall", "-Wno-unused-function",
     f"-I{INCLUDE}",
 ]

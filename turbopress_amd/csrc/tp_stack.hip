@@ -7,27 +7,50 @@
 // latency chain ends, so here one launch streams the whole list of linears:
 //
 //   * work = "blocks" of 8 row tiles x the full K range of one linear, handed
-//     to persistent workgroups by an atomic ticket (self-resetting);
-//   * a block walks K in chunks of 2 units (512 columns): per chunk the
-//     workgroup rotates its slice of x into LDS (tp_tiled_common.h,
-//     stage_z*), every wave decodes and multiplies its tile's units, and the
-//     loads of the next chunk are already in flight;
+//     to persistent workgroups by an atomic ticket (self-resetting), in a
+//     schedule stored in the plan (largest K first when unordered, so the
+//     launch does not end on a long block);
 //   * full-K blocks need no split-K reduction: each wave writes its 16 rows;
 //   * optional phase ordering: linears carry a phase index and, when
 //     `ordered` is set, a block of phase p starts only after every block of
 //     phase p-1 has finished (bounded wait; on timeout the plan's error flag
 //     is set and the block proceeds, so the kernel always terminates).
+//
+// Batch <= 8 (the decode case) runs two kernels:
+//   1. tcq_stack_rotate_kernel: z = blockFWHT(x * rot_scale) / sqrt(hb) of
+//      every linear into the plan's z buffer (fp16, zero past d) -- a few
+//      MB, read back from L2/MALL;
+//   2. tcq_stack_slot_kernel: a wave streams its tile's path/member words
+//      and z with buffer loads, two units ahead, and never synchronises with
+//      the other waves inside a block.  At batch <= 8 only `batch` of the 16
+//      MFMA B columns carry data, so the columns are split into 16/SB "slots"
+//      of SB batch rows: one 16-byte z load per lane feeds 16/SB MFMAs (MFMA
+//      i reads its activations from slot i % (16/SB) and accumulates into its
+//      own accumulator); the valid column of each accumulator is summed
+//      across slots once per block.  The LDS then only serves the codebook
+//      pair table, whose lookups bound the kernel's issue rate.
+// Batch 9..32 runs tcq_stack_lds_kernel: the workgroup rotates each
+// 512-column chunk of x into LDS and all waves read it as B operands.
 #include "tp_tiled_common.h"
+
+#include <algorithm>
+#include <type_traits>
+#include <vector>
 
 namespace tp {
 
 constexpr int kStackMaxPhases = 4096;
+constexpr int kStackMaxLinears = 4096;       // schedule entries: (linear << 20) | block
+constexpr int kStackBlockBits = 20;
+constexpr int kSlotMaxBatch = 8;             // batches up to this use the slot kernel
 
 // Plan layout (device memory):
-//   [0, 64)            StackCounters  -- written by the kernel (atomics)
-//   [64, ...)          StackInfo, LinearDesc[n_lin], prefix[n_lin+1],
-//                      lphase[n_lin], pblocks[n_phases]  -- read-only
-//   [pdone offset, ..) pdone[n_phases] -- written by the kernel (atomics)
+//   [0, 64)             StackCounters  -- written by the kernels (atomics)
+//   [64, ...)           StackInfo, LinearDesc[n_lin], prefix[n_lin+1],
+//                       lphase[n_lin], pblocks[n_phases], sched_ordered[total],
+//                       sched_unordered[total], rot_prefix[n_lin+1]  -- read-only
+//   [pdone, ...)        pdone[n_phases] -- written by the kernel (atomics)
+//   [zbuf, ...)         rotated activations, batch <= 8 plans only
 // The read-only part is passed as a separate const __restrict__ argument so
 // its loads go through the scalar cache into SGPRs.
 struct StackCounters {
@@ -42,9 +65,54 @@ struct StackInfo {
   int32_t total_blocks;
   int32_t n_phases;
   int32_t batch;
-  int64_t pdone_offset;   // byte offset of pdone from the plan start
-  int64_t reserved;
+  int32_t n_rot;          // rotation tiles (batch * 4096-column tiles per linear) when the plan has a z buffer
+  int32_t min_g4;         // shortest K of the plan in 256-column units
+  int64_t zbuf_bytes;
 };
+
+struct StackLayout {
+  size_t lin, prefix, lphase, pblocks, sched_o, sched_u, rot_prefix, pdone, zbuf, total;
+};
+
+constexpr size_t kStackRO = sizeof(StackCounters);
+
+// Reads of the plan's read-only part through the constant address space:
+// the plan does not change during a launch, so wave-uniform reads become
+// scalar loads (a vector load would make every value derived from it
+// per-lane, and its wait would also drain the weight loads in flight).
+#define TP_CONST __attribute__((address_space(4)))
+template <typename T>
+__device__ __forceinline__ const TP_CONST T& cread(const T* p) {
+  return *(const TP_CONST T*)p;
+}
+
+__host__ __device__ inline StackLayout stack_layout(int n_lin, int n_phases, int total_blocks,
+                                                    int64_t zbuf_bytes) {
+  StackLayout p;
+  size_t o = kStackRO + sizeof(StackInfo);
+  p.lin = o;
+  o += sizeof(LinearDesc) * (size_t)n_lin;
+  p.prefix = o;
+  o += sizeof(int32_t) * (size_t)(n_lin + 1);
+  p.lphase = o;
+  o += sizeof(int32_t) * (size_t)n_lin;
+  p.pblocks = o;
+  o += sizeof(int32_t) * (size_t)n_phases;
+  p.sched_o = o;
+  o += sizeof(int32_t) * (size_t)total_blocks;
+  p.sched_u = o;
+  o += sizeof(int32_t) * (size_t)total_blocks;
+  p.rot_prefix = o;
+  o += sizeof(int32_t) * (size_t)(n_lin + 1);
+  o = (o + 63) & ~(size_t)63;
+  p.pdone = o;
+  o += sizeof(uint32_t) * (size_t)n_phases;
+  o = (o + 255) & ~(size_t)255;
+  p.zbuf = o;
+  o += (size_t)zbuf_bytes;
+  p.total = (o + 255) & ~(size_t)255;
+  return p;
+}
 
 struct StackRO {  // views into the read-only part
   const StackInfo* info;
@@ -52,41 +120,556 @@ struct StackRO {  // views into the read-only part
   const int32_t* prefix;   // [n_lin + 1] first block of each linear
   const int32_t* lphase;   // [n_lin]
   const int32_t* pblocks;  // [n_phases] blocks per phase
+  const int32_t* sched_o;  // [total] (linear << 20) | block, phase order
+  const int32_t* sched_u;  // [total] same blocks, longest K first
+  const int32_t* rot_prefix;
+  size_t pdone;            // byte offset of pdone from the plan start
+  size_t zbuf;             // byte offset of the z buffer from the plan start
 };
-
-constexpr size_t kStackRO = sizeof(StackCounters);
-
-__host__ __device__ inline size_t stack_plan_offsets(int n_lin, int n_phases, size_t* o_lin, size_t* o_prefix,
-                                                     size_t* o_lphase, size_t* o_pblocks, size_t* o_pdone) {
-  size_t o = kStackRO + sizeof(StackInfo);
-  *o_lin = o;
-  o += sizeof(LinearDesc) * (size_t)n_lin;
-  *o_prefix = o;
-  o += sizeof(int32_t) * (size_t)(n_lin + 1);
-  *o_lphase = o;
-  o += sizeof(int32_t) * (size_t)n_lin;
-  *o_pblocks = o;
-  o += sizeof(int32_t) * (size_t)n_phases;
-  o = (o + 63) & ~(size_t)63;
-  *o_pdone = o;
-  o += sizeof(uint32_t) * (size_t)n_phases;
-  return (o + 255) & ~(size_t)255;
-}
 
 // `ro` points at plan + kStackRO.
 __device__ inline StackRO stack_ro(const char* __restrict__ ro) {
   const StackInfo* info = reinterpret_cast<const StackInfo*>(ro);
-  size_t a, b, c, d, e;
-  stack_plan_offsets(info->n_lin, info->n_phases, &a, &b, &c, &d, &e);
+  const TP_CONST StackInfo& ci = cread(info);
+  const StackLayout l = stack_layout(ci.n_lin, ci.n_phases, ci.total_blocks, ci.zbuf_bytes);
   StackRO v;
   v.info = info;
-  v.lin = reinterpret_cast<const LinearDesc*>(ro + (a - kStackRO));
-  v.prefix = reinterpret_cast<const int32_t*>(ro + (b - kStackRO));
-  v.lphase = reinterpret_cast<const int32_t*>(ro + (c - kStackRO));
-  v.pblocks = reinterpret_cast<const int32_t*>(ro + (d - kStackRO));
+  v.lin = reinterpret_cast<const LinearDesc*>(ro + (l.lin - kStackRO));
+  v.prefix = reinterpret_cast<const int32_t*>(ro + (l.prefix - kStackRO));
+  v.lphase = reinterpret_cast<const int32_t*>(ro + (l.lphase - kStackRO));
+  v.pblocks = reinterpret_cast<const int32_t*>(ro + (l.pblocks - kStackRO));
+  v.sched_o = reinterpret_cast<const int32_t*>(ro + (l.sched_o - kStackRO));
+  v.sched_u = reinterpret_cast<const int32_t*>(ro + (l.sched_u - kStackRO));
+  v.rot_prefix = reinterpret_cast<const int32_t*>(ro + (l.rot_prefix - kStackRO));
+  v.pdone = l.pdone;
+  v.zbuf = l.zbuf;
   return v;
 }
 
+// Bounded wait of one thread until every block of phase ph - 1 has finished.
+__device__ inline void wait_phase(const StackRO& P, uint32_t* pdone, StackCounters* C, int ph,
+                                  int spin_limit) {
+  const uint32_t need = (uint32_t)cread(P.pblocks + ph - 1);
+  int spins = 0;
+  while (__hip_atomic_load(&pdone[ph - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
+    if (++spins > spin_limit) {
+      atomicExch(&C->error, 1u);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(8);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 1. rotation of every linear's input into the plan's z buffer (batch <= 8)
+// ---------------------------------------------------------------------------
+// One workgroup of 256 threads transforms a tile of up to 4096 columns of
+// one batch row (tiles start at multiples of 4096, so a Hadamard block of at
+// most 4096 never straddles two tiles).  Thread t holds columns 16t..16t+15:
+// butterflies at distance 1..8 run in registers, 16..512 across lanes,
+// 1024 and 2048 as one radix-4 step through LDS -- the stage order of the
+// reference's transform (distance 1, 2, 4, ... then one division by
+// sqrt(block)), all in fp32, z rounded to fp16 once.  A block larger than
+// 4096 (H_hb = H_(hb/4096) (x) H_4096) first sums its 4096-column sub-tiles
+// with the signs of the tile's row of H_(hb/4096).
+constexpr int kRotTile = 4096;
+constexpr int kRotThreads = 256;
+constexpr int kRotEPT = kRotTile / kRotThreads;  // 16
+
+__host__ __device__ inline int rot_tiles(int G4) { return (G4 * kChunkCols + kRotTile - 1) / kRotTile; }
+
+__device__ __forceinline__ void load16(const uint16_t* p, float v[kRotEPT], int valid_groups) {
+#pragma unroll
+  for (int g = 0; g < kRotEPT / 4; ++g) {
+    float t[4] = {0.f, 0.f, 0.f, 0.f};
+    if (g < valid_groups) unpack4h(gld2(p + 4 * g), t);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * g + e] = t[e];
+  }
+}
+
+__global__ void __launch_bounds__(kRotThreads)
+tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
+  __shared__ float ex[kRotTile];
+  const StackRO P = stack_ro(plan_ro);
+  const int n_rot = P.info->n_rot;
+  const int n_lin = P.info->n_lin;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  for (int item = blockIdx.x; item < n_rot; item += gridDim.x) {
+    int lo = 0, hi = n_lin - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (P.rot_prefix[mid] <= item) lo = mid; else hi = mid - 1;
+    }
+    const int li = __builtin_amdgcn_readfirstlane(lo);
+    const LinearDesc L = P.lin[li];
+    const int ntiles = rot_tiles(L.G4);
+    const int local = item - P.rot_prefix[li];
+    const int b = local / ntiles, k = local - b * ntiles;
+    const int c0 = k * kRotTile + tid * kRotEPT;      // first column of this thread
+    const int hb = L.hb;
+    const uint16_t* xr = L.x + (size_t)b * L.ldx;
+    float v[kRotEPT];
+    if (hb <= kRotTile) {
+      // d is a multiple of 4: 4-column groups are wholly inside or outside.
+      const int groups = max(0, min(kRotEPT / 4, (L.d - c0) / 4));
+      float rv[kRotEPT];
+      load16(xr + c0, v, groups);
+      load16(L.rs + c0, rv, groups);
+#pragma unroll
+      for (int e = 0; e < kRotEPT; ++e) v[e] *= rv[e];
+    } else {
+      const int cb = k * kRotTile;
+      const int base = cb - cb % hb, o = (cb % hb) / kRotTile;
+#pragma unroll
+      for (int e = 0; e < kRotEPT; ++e) v[e] = 0.f;
+      for (int i = 0; i < hb / kRotTile; ++i) {
+        const int c = base + i * kRotTile + tid * kRotEPT;
+        float xv[kRotEPT], rv[kRotEPT];
+        load16(xr + c, xv, kRotEPT / 4);
+        load16(L.rs + c, rv, kRotEPT / 4);
+        const bool neg = __popc(i & o) & 1;
+#pragma unroll
+        for (int e = 0; e < kRotEPT; ++e) v[e] += neg ? -(xv[e] * rv[e]) : xv[e] * rv[e];
+      }
+    }
+    const int hmax = hb < kRotTile ? hb : kRotTile;
+#pragma unroll
+    for (int h = 1; h < kRotEPT; h <<= 1) {
+      if (h >= hmax) break;
+#pragma unroll
+      for (int e = 0; e < kRotEPT; ++e) {
+        if ((e & h) == 0) {
+          const float a = v[e], c = v[e + h];
+          v[e] = a + c;
+          v[e + h] = a - c;
+        }
+      }
+    }
+#pragma unroll
+    for (int sft = 0; sft < 6; ++sft) {
+      if ((kRotEPT << sft) >= hmax) break;
+      const bool upper = (lane >> sft) & 1;
+#pragma unroll
+      for (int e = 0; e < kRotEPT; ++e) {
+        const float p = __shfl_xor(v[e], 1 << sft, 64);
+        v[e] = upper ? p - v[e] : v[e] + p;
+      }
+    }
+    if (hmax > 1024) {  // distances 1024 (and 2048): wave bits of the column
+      __syncthreads();  // the previous item's reads of ex are done
+#pragma unroll
+      for (int e = 0; e < kRotEPT; ++e) ex[tid * kRotEPT + e] = v[e];
+      __syncthreads();
+      const int i0 = (lane * kRotEPT) & 1023;
+      if (hmax == 2048) {
+        const int w2 = wave & 1;
+#pragma unroll
+        for (int e = 0; e < kRotEPT; ++e) {
+          const float p = ex[(wave ^ 1) * 1024 + i0 + e];
+          v[e] = w2 ? p - v[e] : v[e] + p;
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < kRotEPT; ++e) {
+          const float u0 = ex[i0 + e], u1 = ex[1024 + i0 + e], u2 = ex[2048 + i0 + e], u3 = ex[3072 + i0 + e];
+          // natural-order H_4 row `wave`: stage 1024 then stage 2048
+          const float s01 = (wave & 1) ? u0 - u1 : u0 + u1;
+          const float s23 = (wave & 1) ? u2 - u3 : u2 + u3;
+          v[e] = (wave & 2) ? s01 - s23 : s01 + s23;
+        }
+      }
+    }
+    const int zld = L.G4 * kChunkCols;
+    uint16_t* zr = L.z + (size_t)b * zld;
+#pragma unroll
+    for (int g = 0; g < kRotEPT / 4; ++g) {
+      if (c0 + 4 * g >= zld) break;
+      const u32x2_t w = {(uint32_t)f2h(v[4 * g] / L.hdiv) | ((uint32_t)f2h(v[4 * g + 1] / L.hdiv) << 16),
+                         (uint32_t)f2h(v[4 * g + 2] / L.hdiv) | ((uint32_t)f2h(v[4 * g + 3] / L.hdiv) << 16)};
+      *(TP_GLOBAL u32x2_t*)(zr + c0 + 4 * g) = w;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. slot kernel (batch <= 8)
+// ---------------------------------------------------------------------------
+constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferFlags);
+}
+
+__device__ __forceinline__ u32x2_t gld2v(const char* p) { return *(const TP_GLOBAL u32x2_t*)p; }
+
+template <int MW> struct MemberBuf;
+template <> struct MemberBuf<2> {
+  typedef u32x2_t type;
+  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, v, s, 0);
+  }
+};
+template <> struct MemberBuf<4> {
+  typedef u32x4_t type;
+  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, v, s, 0);
+  }
+};
+
+template <int MW> struct MemberLoad;
+template <> struct MemberLoad<2> {
+  typedef u32x2_t type;
+  static __device__ __forceinline__ type load(const char* p) { return *(const TP_GLOBAL u32x2_t*)p; }
+};
+template <> struct MemberLoad<4> {
+  typedef u32x4_t type;
+  static __device__ __forceinline__ type load(const char* p) { return *(const TP_GLOBAL u32x4_t*)p; }
+};
+
+// Loads of one unit of one lane.
+template <int MW, int NZ>
+struct UnitRegs {
+  u32x2_t X;
+  typename MemberBuf<MW>::type M;
+  u32x4_t Z[NZ];
+};
+
+// Column (inside a 64-column segment) of the first of the 8 K positions of
+// MFMA i of a unit: word x = i / 4 holds columns 16x..16x+15 and
+// 32+16x..32+16x+15; MFMA j = i % 4 takes 8 of them.
+__host__ __device__ constexpr int mfma_col(int i) {
+  return 16 * (i >> 2) + ((i & 2) ? 32 : 0) + ((i & 1) ? 8 : 0);
+}
+
+// One unit of one wave: decode 64 weights per lane, 8 MFMAs.  Word 1 is
+// decoded first: its previous word is this lane's word 0, so the halo
+// exchange needed by word 0 completes meanwhile.
+template <int KB, int NS, int SB, int MW, int NZ>
+__device__ __forceinline__ void slot_unit(const UnitRegs<MW, NZ>& g, const uint32_t provide, const int lane,
+                                          const uint32_t laneoff, const uint32_t* table, float4_t* acc) {
+  constexpr int SLOTS = 16 / SB;
+  const uint32_t halo = (uint32_t)__shfl((int)provide, (lane + 48) & 63, 64);
+  MemberWords<KB> m[2];
+  if constexpr (KB == 3) {
+    m[0].a = g.M[0]; m[0].b = g.M[1]; m[1].a = g.M[2]; m[1].b = g.M[3];
+  } else {
+    m[0].w = g.M[0]; m[1].w = g.M[1];
+  }
+#pragma unroll
+  for (int xi = 0; xi < 2; ++xi) {
+    const int x = 1 - xi;
+    u32x4_t A[4];
+    if (x == 1) {
+      decode_word<KB, NS>(g.X[1], g.X[0], m[1], table, laneoff, A);
+    } else {
+      const uint32_t P = ((halo >> 1) & 0x55555555u) | ((g.X[1] << 1) & 0xAAAAAAAAu);
+      decode_word<KB, NS>(g.X[0], P, m[0], table, laneoff, A);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = 4 * x + j;
+      const half8_t b = __builtin_bit_cast(half8_t, g.Z[i / SLOTS]);
+      acc[i % SLOTS] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, A[j]), b,
+                                                             acc[i % SLOTS], 0, 0, 0);
+    }
+  }
+}
+
+// Read-only state of one wave of the slot kernel.
+struct SlotEnv {
+  StackRO P;
+  const int32_t* sched;
+  const char* zbuf;
+  StackCounters* C;
+  uint32_t* pdone;
+  const uint32_t* table;
+  __amdgpu_buffer_rsrc_t zrs;   // the whole z buffer
+  int total, batch, wave, lane, q, slot, bb, ordered, spin_limit, tid;
+  uint32_t laneoff, pv, mv, slot_bit;
+};
+
+// A block of the stream as one wave sees it (wave-uniform).
+struct BlockInfo {
+  int li;
+  int t;    // row tile of this wave
+  int G4;   // units along K; 0 when the ticket is past the end of the work
+};
+
+__device__ __forceinline__ BlockInfo stream_info(const SlotEnv& E, int blk) {
+  BlockInfo b;
+  const bool valid = blk < E.total;
+  const int e = cread(E.sched + (valid ? blk : 0));
+  b.li = __builtin_amdgcn_readfirstlane(e >> kStackBlockBits);
+  b.t = (e & ((1 << kStackBlockBits) - 1)) * kWavesPerGroup + E.wave;
+  b.G4 = valid ? cread(E.P.lin + b.li).G4 : 0;
+  return b;
+}
+
+// Where the stream loads from: buffer descriptors of one block's tile of
+// path/member words, the linear's z rows and this lane's z offsets.
+template <int NZ>
+struct LoadCtx {
+  __amdgpu_buffer_rsrc_t prs, mrs;
+  uint32_t zoff;       // byte offset of the linear's z rows in the z buffer
+  uint32_t zv[NZ];     // lane offsets inside the z rows (per-lane)
+  int G4;
+};
+
+template <int MW, int SB, int NZ>
+__device__ __forceinline__ LoadCtx<NZ> stream_ctx(const SlotEnv& E, const BlockInfo& b) {
+  constexpr int SLOTS = 16 / SB;
+  const TP_CONST LinearDesc& L = cread(E.P.lin + b.li);
+  const int tt = b.t < L.T ? b.t : 0;
+  LoadCtx<NZ> c;
+  const uint32_t unit_p = 4u * kTileRows * 8u, unit_m = 4u * kTileRows * MW * 4u;
+  c.prs = buffer_rsrc(reinterpret_cast<const char*>(L.path) + (size_t)tt * L.G * (kTileRows * 2 * 4),
+                      (uint32_t)L.G4 * unit_p);
+  c.mrs = buffer_rsrc(reinterpret_cast<const char*>(L.member) + (size_t)tt * L.G * (kTileRows * MW * 4),
+                      (uint32_t)L.G4 * unit_m);
+  c.zoff = (uint32_t)(reinterpret_cast<const char*>(L.z) - E.zbuf);
+  const uint32_t zld = (uint32_t)L.G4 * kChunkCols;
+#pragma unroll
+  for (int l = 0; l < NZ; ++l) {
+    const int i = l * SLOTS + E.slot;  // the MFMA whose B column this lane supplies
+    c.zv[l] = E.bb < E.batch ? ((uint32_t)E.bb * zld + (uint32_t)(E.q * kSegCols + mfma_col(i))) * 2u
+                             : kOutOfRange;  // out of range: zeros, no memory traffic
+  }
+  c.G4 = b.G4;
+  return c;
+}
+
+template <int MW, int NZ>
+__device__ __forceinline__ UnitRegs<MW, NZ> stream_load(const SlotEnv& E, const LoadCtx<NZ>& c, int gu) {
+  constexpr uint32_t unit_p = 4u * kTileRows * 8u;        // path bytes per unit
+  constexpr uint32_t unit_m = 4u * kTileRows * MW * 4u;   // member bytes per unit
+  constexpr uint32_t unit_z = kChunkCols * 2u;            // z bytes per unit and batch row
+  UnitRegs<MW, NZ> g;
+  g.X = __builtin_amdgcn_raw_buffer_load_b64(c.prs, E.pv, (uint32_t)gu * unit_p, 0);
+  g.M = MemberBuf<MW>::load(c.mrs, E.mv, (uint32_t)gu * unit_m);
+  // (uniform by construction; readfirstlane keeps it in a scalar register
+  // when the compiler merges it with per-lane values)
+  const uint32_t zs = (uint32_t)__builtin_amdgcn_readfirstlane((int)(c.zoff + (uint32_t)gu * unit_z));
+#pragma unroll
+  for (int l = 0; l < NZ; ++l) g.Z[l] = __builtin_amdgcn_raw_buffer_load_b128(E.zrs, c.zv[l], zs, 0);
+  return g;
+}
+
+// Row scales of the lane's rows 4q..4q+3 of a block (range-checked: rows
+// past n read 0 and are never written).
+struct Scales4 { uint32_t v[4]; };
+__device__ __forceinline__ Scales4 stream_scales(const SlotEnv& E, const BlockInfo& b) {
+  const TP_CONST LinearDesc& L = cread(E.P.lin + b.li);
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(L.scales, (uint32_t)L.n * 2u);
+  const uint32_t off = (uint32_t)(b.t * kTileRows + 4 * E.q) * 2u;
+  Scales4 s;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s.v[i] = __builtin_amdgcn_raw_buffer_load_b16(srs, off + 2u * i, 0, 0);
+  return s;
+}
+
+__device__ __forceinline__ void stream_phase_wait(const SlotEnv& E, int li) {
+  if (!E.ordered) return;
+  const int ph = cread(E.P.lphase + li);
+  if (ph > 0) {
+    if (E.tid == 0) wait_phase(E.P, E.pdone, E.C, ph, E.spin_limit);
+    __syncthreads();
+  }
+}
+
+// The stream of one wave (see tcq_stack_slot_kernel) with D register sets.
+// Blocks of the workgroup: cur (being decoded), nxt (known: its ticket was
+// broadcast at the previous block end) and the one after (claimed by thread
+// 0, published at the end of cur).  The load cursor runs D - 1 units ahead
+// of the decoder, in cur or in nxt.
+template <int KB, int NS, int SB, int D>
+__device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1, uint32_t pend, int* s_tk) {
+  constexpr int MW = member_words(KB);
+  constexpr int SLOTS = 16 / SB;
+  constexpr int NZ = 8 / SLOTS;
+  BlockInfo cur = stream_info(E, blk0);
+  BlockInfo nxt = stream_info(E, blk1);
+  if (cur.G4 == 0) return;
+  LoadCtx<NZ> lc = stream_ctx<MW, SB, NZ>(E, cur);
+  bool lnext = false;           // the load cursor is in nxt
+  int lgu = 0;                  // next unit to load
+  int pgu = 0;                  // next unit of cur to decode
+  int bseq = 0;                 // blocks finished by this workgroup
+  UnitRegs<MW, NZ> R[D];
+  float4_t acc[SLOTS];
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) acc[s] = float4_t{0.f, 0.f, 0.f, 0.f};
+  uint32_t x1_last = 0;
+  Scales4 sc = stream_scales(E, cur);
+  stream_phase_wait(E, cur.li);
+
+  // Load the cursor's unit into set k, then advance the cursor; at the end
+  // of cur it moves into nxt, at the end of nxt (or of the work) it stays and
+  // reloads its unit (in range, never decoded).
+#define TP_STREAM_ISSUE(k)                                     \
+  do {                                                         \
+    R[k] = stream_load<MW, NZ>(E, lc, lgu);                    \
+    if (lgu + 1 < lc.G4) {                                     \
+      ++lgu;                                                   \
+    } else if (!lnext && nxt.G4 > 0) {                         \
+      lc = stream_ctx<MW, SB, NZ>(E, nxt);                     \
+      lnext = true;                                            \
+      lgu = 0;                                                 \
+    }                                                          \
+  } while (0)
+
+#pragma unroll
+  for (int k = 0; k < D - 1; ++k) TP_STREAM_ISSUE(k);
+
+  for (;;) {
+#pragma unroll
+    for (int k = 0; k < D; ++k) {
+      TP_STREAM_ISSUE((k + D - 1) % D);
+      // Halo: word 1 of the previous segment comes from the lane 16 below
+      // (K block q-1); lanes of K block 0 take the previous unit's last
+      // segment (from lanes of K block 3, carried in x1_last); zero at a
+      // row start.
+      const uint32_t provide = (E.q == 3) ? (pgu == 0 ? 0u : x1_last) : R[k].X[1];
+      slot_unit<KB, NS, SB, MW, NZ>(R[k], provide, E.lane, E.laneoff, E.table, acc);
+      x1_last = R[k].X[1];
+      if (++pgu == cur.G4) {
+        // Block end: accumulator `slot` holds this lane's valid column; sum
+        // the slots of each batch row, lanes of slot 0 write rows 4q..4q+3.
+        const TP_CONST LinearDesc& L = cread(E.P.lin + cur.li);
+        // v = acc[slot], as a masked sum (per-slot lane compares would stay
+        // live in scalar registers across the loop)
+        float4_t v = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) {
+          const float m = (float)__builtin_amdgcn_ubfe(E.slot_bit, (uint32_t)s, 1u);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(acc[s][i], m, v[i]);
+        }
+#pragma unroll
+        for (int w = SB; w < 16; w <<= 1)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], w, 64);
+        if (cur.t < L.T && E.slot == 0 && E.bb < E.batch) {
+          const int row0 = cur.t * kTileRows + 4 * E.q;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int row = row0 + i;
+            if (row >= L.n) continue;
+            uint16_t out = f2h(v[i] * h2f((uint16_t)sc.v[i]));
+            if (L.bias) out = f2h(h2f(out) + h2f(gld(L.bias + row)));
+            gst(L.y + (size_t)E.bb * L.ldy + row, out);
+          }
+        }
+#pragma unroll
+        for (int s = 0; s < SLOTS; ++s) acc[s] = float4_t{0.f, 0.f, 0.f, 0.f};
+        if (E.ordered) {
+          __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          __syncthreads();
+          if (E.tid == 0) atomicAdd(&E.pdone[cread(E.P.lphase + cur.li)], 1u);
+        }
+        if (nxt.G4 == 0) return;
+        // nxt becomes cur; the ticket claimed during this block names the
+        // block after it (double-buffered slot: a slot is rewritten two
+        // block ends later, after every wave has read it).
+        if (E.tid == 0) s_tk[bseq & 1] = (int)pend;
+        __syncthreads();
+        const int blk = __builtin_amdgcn_readfirstlane(s_tk[bseq & 1]);
+        ++bseq;
+        if (E.tid == 0 && blk < E.total) pend = atomicAdd(&E.C->ticket, 1u);
+        cur = nxt;
+        nxt = stream_info(E, blk);
+        lnext = false;  // the load cursor is in the new cur
+        pgu = 0;
+        sc = stream_scales(E, cur);
+        stream_phase_wait(E, cur.li);
+      }
+    }
+  }
+#undef TP_STREAM_ISSUE
+}
+
+constexpr int kStreamDepth = 4;  // unit register sets of the stream (plans whose K >= 3 units)
+
+// Persistent stream of units: the workgroup walks its blocks (tickets claimed
+// two blocks ahead) and every wave streams its tile's units with D - 1 units
+// of loads in flight, across block boundaries (the next block's first units
+// load while the current block's last units are decoded).  With every block
+// at least D - 1 units long (D is picked from the plan's shortest K), the
+// load cursor never runs past the next block.  Every load is issued
+// unconditionally (after the last block, an in-range unit is reloaded and
+// never used), so the number of loads in flight is the same on every path
+// and each wait covers the oldest register set only.
+template <int KB, int NS, int SB>
+__global__ void __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(4)))
+tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
+                      const uint16_t* __restrict__ codebook, int ordered, int spin_limit) {
+  __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
+  __shared__ int s_tk[2];
+  constexpr int MW = member_words(KB);
+  SlotEnv E;
+  E.P = stack_ro(plan_ro);
+  E.total = cread(E.P.info).total_blocks;
+  E.batch = cread(E.P.info).batch;
+  E.zbuf = plan_rw + E.P.zbuf;
+  E.C = reinterpret_cast<StackCounters*>(plan_rw);
+  E.pdone = reinterpret_cast<uint32_t*>(plan_rw + E.P.pdone);
+  if (E.batch > SB || cread(E.P.info).n_rot <= 0) {  // not a plan for this kernel
+    if (threadIdx.x == 0 && blockIdx.x == 0) atomicExch(&E.C->error, 2u);
+    return;
+  }
+  E.sched = ordered ? E.P.sched_o : E.P.sched_u;
+  E.table = table;
+  E.ordered = ordered;
+  E.spin_limit = spin_limit;
+  E.tid = threadIdx.x;
+  E.lane = E.tid & 63;
+  E.wave = __builtin_amdgcn_readfirstlane(E.tid >> 6);
+  const int r = E.lane & 15;
+  E.q = E.lane >> 4;
+  E.slot = r / SB;
+  E.bb = r % SB;
+  E.slot_bit = 1u << E.slot;
+  E.laneoff = lane_offsets<KB>(E.lane);
+  E.pv = (uint32_t)(E.q * kTileRows + r) * 8u;        // path byte offset in a unit
+  E.mv = (uint32_t)(E.q * kTileRows + r) * MW * 4u;   // member byte offset in a unit
+  E.zrs = buffer_rsrc(plan_rw + E.P.zbuf, (uint32_t)cread(E.P.info).zbuf_bytes);
+  const uint32_t cb_lane = gld(codebook + (E.lane & ((2 << KB) - 1)));
+
+  if (E.tid == 0) {
+    s_tk[0] = (int)atomicAdd(&E.C->ticket, 1u);
+    s_tk[1] = (int)atomicAdd(&E.C->ticket, 1u);
+  }
+  build_pair_table_lanes<KB>(table, cb_lane, E.tid, kGroupThreads);
+  __syncthreads();
+  const int blk0 = __builtin_amdgcn_readfirstlane(s_tk[0]);
+  const int blk1 = __builtin_amdgcn_readfirstlane(s_tk[1]);
+  uint32_t pend = 0;  // thread 0: ticket of the block after blk1
+  if (E.tid == 0) pend = atomicAdd(&E.C->ticket, 1u);
+  // Register sets: 4 for 4 z columns per lane set (SB = 4), 2 for SB = 8
+  // (four z loads per unit); 2 when a block is shorter than the pipeline.
+  constexpr int DMAX = SB <= 4 ? kStreamDepth : 2;
+  if (cread(E.P.info).min_g4 >= DMAX - 1)
+    slot_stream<KB, NS, SB, DMAX>(E, blk0, blk1, pend, s_tk);
+  else
+    slot_stream<KB, NS, SB, 2>(E, blk0, blk1, pend, s_tk);
+
+  // The last workgroup out resets the counters for the next launch.
+  if (E.tid == 0) {
+    const uint32_t ex = atomicAdd(&E.C->exited, 1u);
+    if (ex == gridDim.x - 1) {
+      for (int p = 0; p < cread(E.P.info).n_phases; ++p) atomicExch(&E.pdone[p], 0u);
+      atomicExch(&E.C->ticket, 0u);
+      atomicExch(&E.C->exited, 0u);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. LDS-staged kernel (batch 9..32)
+// ---------------------------------------------------------------------------
 // Path/member words of one chunk (kMaxUnitsPerBlock units) of one lane.
 template <int MW>
 struct ChunkRegs {
@@ -96,13 +679,12 @@ struct ChunkRegs {
 
 template <int MW>
 __device__ __forceinline__ ChunkRegs<MW> load_chunk(const LinearDesc& L, const uint32_t* pt, const uint32_t* mt,
-                                                     int ch, bool active, int q, int r) {
+                                                     int ch, int q, int r) {
   // Branch-free: units past the block's K range (and inactive waves, whose
   // pointers address tile 0) reload unit 0 of the chunk; they are never used.
   ChunkRegs<MW> c;
   const int gu0 = ch * kMaxUnitsPerBlock;
   const int ngu = min(kMaxUnitsPerBlock, L.G4 - gu0);
-  (void)active;
 #pragma unroll
   for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
     const int g = 4 * (gu0 + (u < ngu ? u : 0)) + q;
@@ -114,95 +696,69 @@ __device__ __forceinline__ ChunkRegs<MW> load_chunk(const LinearDesc& L, const u
 }
 
 template <int KB, int NS, int NBT>
-__global__ void __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(NBT == 1 ? 4 : 2)))
-tcq_stack_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
-                 const uint16_t* __restrict__ codebook, int ordered, int spin_limit, int zrows) {
+__global__ void __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(2)))
+tcq_stack_lds_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
+                     const uint16_t* __restrict__ codebook, int ordered, int spin_limit, int zrows) {
   __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
   extern __shared__ __attribute__((aligned(16))) uint16_t zl[];
   __shared__ int s_next;
   constexpr int MW = member_words(KB);
   // Sizes come from the plan itself, never from the caller.
   const StackRO P = stack_ro(plan_ro);
-  const int n_lin = P.info->n_lin;
-  const int n_phases = P.info->n_phases;
   const int batch = P.info->batch;
   const int total = P.info->total_blocks;
   StackCounters* C = reinterpret_cast<StackCounters*>(plan_rw);
-  uint32_t* pdone = reinterpret_cast<uint32_t*>(plan_rw + P.info->pdone_offset);
+  uint32_t* pdone = reinterpret_cast<uint32_t*>(plan_rw + P.pdone);
   if (batch > 16 * NBT || batch > zrows) {  // staged z rows would not fit: refuse uniformly
     if (threadIdx.x == 0 && blockIdx.x == 0) atomicExch(&C->error, 2u);
     return;
   }
+  const int32_t* sched = ordered ? P.sched_o : P.sched_u;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int r = lane & 15;
   const int q = lane >> 4;
-  const uint32_t laneoff = (uint32_t)lane << 2;
+  const uint32_t laneoff = lane_offsets<KB>(lane);
   const uint32_t cb_lane = gld(codebook + (lane & ((2 << KB) - 1)));
 
   if (tid == 0) s_next = (int)atomicAdd(&C->ticket, 1u);
   build_pair_table_lanes<KB>(table, cb_lane, tid, kGroupThreads);
   __syncthreads();
   // The ticket travels through LDS; make its uniformity explicit so that the
-  // descriptor reads below become scalar loads (vector loads would be followed
-  // by waits that also drain the weight prefetches in flight).
+  // descriptor reads below become scalar loads.
   int blk = __builtin_amdgcn_readfirstlane(s_next);
 
   while (blk < total) {
-    // Linear of this block: last li with prefix[li] <= blk (uniform).
-    int lo = 0, hi = n_lin - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (P.prefix[mid] <= blk) lo = mid; else hi = mid - 1;
-    }
-    const int li = __builtin_amdgcn_readfirstlane(lo);
+    const int e = sched[blk];
+    const int li = __builtin_amdgcn_readfirstlane(e >> kStackBlockBits);
+    const int lb = e & ((1 << kStackBlockBits) - 1);
     const LinearDesc L = P.lin[li];  // copied to registers once per block
-    const int t = (blk - P.prefix[li]) * kWavesPerGroup + wave;
+    const int t = lb * kWavesPerGroup + wave;
     const bool active = t < L.T;
     const int nch = (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock;
     const uint32_t* pt = L.path + (size_t)(active ? t : 0) * L.G * (kTileRows * 2);
     const uint32_t* mt = L.member + (size_t)(active ? t : 0) * L.G * (kTileRows * MW);
 
-    // Claim the next block now; its index is needed only after this one.
     uint32_t next_ticket = 0;
     if (tid == 0) next_ticket = atomicAdd(&C->ticket, 1u);
-
     if (ordered) {
       const int ph = P.lphase[li];
       if (ph > 0) {
-        if (tid == 0) {
-          const uint32_t need = (uint32_t)P.pblocks[ph - 1];
-          int spins = 0;
-          while (__hip_atomic_load(&pdone[ph - 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < need) {
-            if (++spins > spin_limit) {
-              atomicExch(&C->error, 1u);
-              break;
-            }
-            __builtin_amdgcn_s_sleep(8);
-          }
-        }
+        if (tid == 0) wait_phase(P, pdone, C, ph, spin_limit);
         __syncthreads();
       }
     }
 
-    // Chunks run ping-pong over two register sets (A, B): a set is refilled
-    // only after its last use, so the prefetched values never need a register
-    // copy (a copy would have to wait for the prefetch to land).
     uint32_t x1_last = 0;
     float4_t acc[NBT];
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
-    auto chunk_body = [&](int ch, const ChunkRegs<MW>& regs, const ZPrefetch& zpf) {
+    auto chunk_body = [&](int ch, const ChunkRegs<MW>& regs) {
       const int gu0 = ch * kMaxUnitsPerBlock;
       const int ngu = min(kMaxUnitsPerBlock, L.G4 - gu0);
-      const bool small = ngu * batch <= kWavesPerGroup && L.hb <= 2 * kChunkCols;
       __syncthreads();  // z of the previous chunk is no longer read
-      if (small) {
-        if (zpf.valid) stage_z_prefetched<true>(L, gu0, batch, zl, wave, lane, zpf);
-      } else {
-        stage_z<true>(L, gu0, ngu, batch, zl, wave, lane);
-      }
+      stage_z<true>(L, gu0, ngu, batch, zl, wave, lane);
       __syncthreads();
       if (active) {
 #pragma unroll
@@ -215,17 +771,13 @@ tcq_stack_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
         }
       }
     };
-    auto ngu_of = [&](int ch) { return ch < nch ? min(kMaxUnitsPerBlock, L.G4 - ch * kMaxUnitsPerBlock) : 0; };
-    ChunkRegs<MW> ra = load_chunk<MW>(L, pt, mt, 0, active, q, r);
-    ZPrefetch za = prefetch_z<true>(L, 0, ngu_of(0), batch, wave, lane);
+    ChunkRegs<MW> ra = load_chunk<MW>(L, pt, mt, 0, q, r);
     for (int ch = 0; ch < nch; ch += 2) {
-      const ChunkRegs<MW> rb = load_chunk<MW>(L, pt, mt, ch + 1 < nch ? ch + 1 : ch, active && ch + 1 < nch, q, r);
-      const ZPrefetch zb = prefetch_z<true>(L, (ch + 1) * kMaxUnitsPerBlock, ngu_of(ch + 1), batch, wave, lane);
-      chunk_body(ch, ra, za);
+      const ChunkRegs<MW> rb = load_chunk<MW>(L, pt, mt, ch + 1 < nch ? ch + 1 : ch, q, r);
+      chunk_body(ch, ra);
       if (ch + 1 >= nch) break;
-      ra = load_chunk<MW>(L, pt, mt, ch + 2 < nch ? ch + 2 : ch, active && ch + 2 < nch, q, r);
-      za = prefetch_z<true>(L, (ch + 2) * kMaxUnitsPerBlock, ngu_of(ch + 2), batch, wave, lane);
-      chunk_body(ch + 1, rb, zb);
+      ra = load_chunk<MW>(L, pt, mt, ch + 2 < nch ? ch + 2 : ch, q, r);
+      chunk_body(ch + 1, rb);
     }
 
     // Full-K epilogue: lane holds rows 4q..4q+3 of its tile for batch column r.
@@ -257,68 +809,125 @@ tcq_stack_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
     blk = __builtin_amdgcn_readfirstlane(s_next);
   }
 
-  // The last workgroup out resets the counters for the next launch.
   if (tid == 0) {
-    const uint32_t e = atomicAdd(&C->exited, 1u);
-    if (e == gridDim.x - 1) {
-      for (int p = 0; p < n_phases; ++p) atomicExch(&pdone[p], 0u);
+    const uint32_t ex = atomicAdd(&C->exited, 1u);
+    if (ex == gridDim.x - 1) {
+      for (int p = 0; p < P.info->n_phases; ++p) atomicExch(&pdone[p], 0u);
       atomicExch(&C->ticket, 0u);
       atomicExch(&C->exited, 0u);
     }
   }
 }
 
-// z staging rows: 8 for batch <= 8 keeps table + z + ticket slot within half
-// of the 160 KiB LDS, so two workgroups share a CU.
-inline int stack_z_rows(int64_t batch) { return batch <= 8 ? 8 : batch <= 16 ? 16 : 32; }
+// z staging rows of the LDS kernel: 16 rows (batch <= 16) keep table + z
+// within 80 KiB (two workgroups per CU); 32 rows need one workgroup per CU.
+inline int stack_z_rows(int64_t batch) { return batch <= 16 ? 16 : 32; }
 
-template <int KB, int NS, int NBT>
-void launch_stack(char* plan, int grid, int64_t batch, const uint16_t* cb, int ordered, int spin_limit,
-                  hipStream_t s) {
-  hipLaunchKernelGGL((tcq_stack_kernel<KB, NS, NBT>), dim3(grid), dim3(kGroupThreads),
-                     (size_t)stack_z_rows(batch) * kZCols * 2, s, (const char*)(plan + kStackRO), plan, cb,
-                     ordered, spin_limit, stack_z_rows(batch));
+inline int slot_batch(int64_t batch) { return batch <= 4 ? 4 : 8; }
+
+template <int KB, int NS>
+int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t* cb, int ordered,
+                int spin_limit, hipStream_t s) {
+  const char* ro = plan + kStackRO;
+  const int cus = device_cu_count();
+  const int per_cu = batch <= 16 ? 2 : 1;
+  const int grid = (int)(total_blocks < (int64_t)cus * per_cu ? total_blocks : (int64_t)cus * per_cu);
+  if (batch <= kSlotMaxBatch) {
+    const int sb = slot_batch(batch);
+    if (sb == 4)
+      hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 4>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
+                         ordered, spin_limit);
+    else
+      hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 8>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
+                         ordered, spin_limit);
+  } else {
+    const int zr = stack_z_rows(batch);
+    const size_t zbytes = (size_t)zr * kZCols * 2;
+    if (batch <= 16)
+      hipLaunchKernelGGL((tcq_stack_lds_kernel<KB, NS, 1>), dim3(grid), dim3(kGroupThreads), zbytes, s, ro, plan,
+                         cb, ordered, spin_limit, zr);
+    else
+      hipLaunchKernelGGL((tcq_stack_lds_kernel<KB, NS, 2>), dim3(grid), dim3(kGroupThreads), zbytes, s, ro, plan,
+                         cb, ordered, spin_limit, zr);
+  }
+  return launch_status();
+}
+
+// Host-side sizes of a stack (validated); zbuf_bytes and n_rot are 0 for batch > 8.
+struct StackSizes {
+  int n_phases;
+  int64_t total_blocks, n_rot, zbuf_bytes, min_g4;
+};
+
+inline int64_t zbuf_linear_bytes(int64_t batch, int64_t G4) { return (batch * G4 * kChunkCols * 2 + 255) & ~(int64_t)255; }
+
+inline int stack_sizes(const tp_stack_linear* linears, int n_linears, int bits, int64_t batch, StackSizes* out) {
+  if (!linears) return TP_ERR_NULL_POINTER;
+  if (n_linears < 1 || n_linears > kStackMaxLinears || batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
+  StackSizes z = {1, 0, 0, 0, INT32_MAX};
+  for (int i = 0; i < n_linears; ++i) {
+    const tp_stack_linear& l = linears[i];
+    if (l.phase < 0 || l.phase >= kStackMaxPhases) return TP_ERR_BAD_DIMS;
+    if (i > 0 && l.phase < linears[i - 1].phase) return TP_ERR_BAD_DIMS;  // phases ascend
+    if (l.phase + 1 > z.n_phases) z.n_phases = l.phase + 1;
+    Geom g;
+    const int st = tiled_geom(l.n, l.d, bits, &g);
+    if (st) return st;
+    const int64_t blocks = (g.T + kWavesPerGroup - 1) / kWavesPerGroup;
+    if (blocks >= (1 << kStackBlockBits)) return TP_ERR_BAD_DIMS;
+    z.total_blocks += blocks;
+    if (g.G4 < z.min_g4) z.min_g4 = g.G4;
+    if (batch <= kSlotMaxBatch) {
+      z.n_rot += batch * rot_tiles((int)g.G4);
+      z.zbuf_bytes += zbuf_linear_bytes(batch, g.G4);
+    }
+  }
+  // z buffer offsets are 32-bit and lanes past the batch read at 2^31: keep it below 2 GiB
+  if (z.total_blocks > INT32_MAX / 2 || z.n_rot > INT32_MAX || z.zbuf_bytes >= ((int64_t)1 << 31))
+    return TP_ERR_BAD_DIMS;
+  *out = z;
+  return TP_OK;
 }
 
 }  // namespace tp
 
 using namespace tp;
 
-extern "C" int64_t tp_stack_plan_bytes(int n_linears, int n_phases) {
-  if (n_linears < 1 || n_phases < 1 || n_phases > kStackMaxPhases) return 0;
-  size_t a, b, c, d, e;
-  return (int64_t)stack_plan_offsets(n_linears, n_phases, &a, &b, &c, &d, &e);
+extern "C" int64_t tp_stack_plan_bytes(const tp_stack_linear* linears, int n_linears, int bits, int64_t batch) {
+  if (bits != 2 && bits != 3) return 0;
+  StackSizes z;
+  if (stack_sizes(linears, n_linears, bits, batch, &z) != TP_OK) return 0;
+  return (int64_t)stack_layout(n_linears, z.n_phases, (int)z.total_blocks, z.zbuf_bytes).total;
 }
 
 extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears, int bits,
                                   int64_t batch, void* plan, int64_t plan_bytes) {
   if (!linears || !plan) return TP_ERR_NULL_POINTER;
-  if (n_linears < 1 || batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
   if (bits != 2 && bits != 3) return TP_ERR_UNSUPPORTED_BITS;
-  int n_phases = 1;
-  for (int i = 0; i < n_linears; ++i) {
-    if (linears[i].phase < 0 || linears[i].phase >= kStackMaxPhases) return TP_ERR_BAD_DIMS;
-    if (i > 0 && linears[i].phase < linears[i - 1].phase) return TP_ERR_BAD_DIMS;  // phases ascend
-    if (linears[i].phase + 1 > n_phases) n_phases = linears[i].phase + 1;
-  }
-  size_t o_lin, o_prefix, o_lphase, o_pdone, o_pblocks;
-  const size_t need = stack_plan_offsets(n_linears, n_phases, &o_lin, &o_prefix, &o_lphase, &o_pblocks, &o_pdone);
-  if (plan_bytes < (int64_t)need) return TP_ERR_WORKSPACE;
+  StackSizes z;
+  int st = stack_sizes(linears, n_linears, bits, batch, &z);
+  if (st) return st;
+  const StackLayout lay = stack_layout(n_linears, z.n_phases, (int)z.total_blocks, z.zbuf_bytes);
+  if (plan_bytes < (int64_t)lay.total) return TP_ERR_WORKSPACE;
   if ((uintptr_t)plan & 255) return TP_ERR_MISALIGNED;
-  char* host = (char*)calloc(1, need);
+  // Everything before the z buffer is written from the host; every run
+  // fills the z buffer before reading it.
+  char* host = (char*)calloc(1, lay.zbuf);
   if (!host) return TP_ERR_HIP;
   StackInfo* h = reinterpret_cast<StackInfo*>(host + kStackRO);
-  LinearDesc* lin = reinterpret_cast<LinearDesc*>(host + o_lin);
-  int32_t* prefix = reinterpret_cast<int32_t*>(host + o_prefix);
-  int32_t* lphase = reinterpret_cast<int32_t*>(host + o_lphase);
-  int32_t* pblocks = reinterpret_cast<int32_t*>(host + o_pblocks);
-  int64_t total = 0;
-  int st = TP_OK;
-  for (int i = 0; i < n_linears && st == TP_OK; ++i) {
+  LinearDesc* lin = reinterpret_cast<LinearDesc*>(host + lay.lin);
+  int32_t* prefix = reinterpret_cast<int32_t*>(host + lay.prefix);
+  int32_t* lphase = reinterpret_cast<int32_t*>(host + lay.lphase);
+  int32_t* pblocks = reinterpret_cast<int32_t*>(host + lay.pblocks);
+  int32_t* sched_o = reinterpret_cast<int32_t*>(host + lay.sched_o);
+  int32_t* sched_u = reinterpret_cast<int32_t*>(host + lay.sched_u);
+  int32_t* rot_prefix = reinterpret_cast<int32_t*>(host + lay.rot_prefix);
+  char* zbuf = reinterpret_cast<char*>(plan) + lay.zbuf;
+  int64_t total = 0, rot = 0, zoff = 0;
+  for (int i = 0; i < n_linears; ++i) {
     const tp_stack_linear& l = linears[i];
     Geom g;
-    st = tiled_geom(l.n, l.d, bits, &g);
-    if (st) break;
+    tiled_geom(l.n, l.d, bits, &g);  // validated by stack_sizes
     if (!l.path_tiled || !l.member_tiled || !l.x || !l.rot_scale || !l.scales || !l.y) {
       st = TP_ERR_NULL_POINTER;
       break;
@@ -341,6 +950,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     L.y = l.y;
     L.ws = nullptr;
     L.cnt = nullptr;
+    L.z = z.zbuf_bytes ? reinterpret_cast<uint16_t*>(zbuf + zoff) : nullptr;
     L.hdiv = (float)__builtin_sqrt((double)hb);
     L.n = (int32_t)l.n;
     L.d = (int32_t)l.d;
@@ -353,52 +963,82 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     L.blocks = (int32_t)((g.T + kWavesPerGroup - 1) / kWavesPerGroup);
     L.hb = (int32_t)hb;
     prefix[i] = (int32_t)total;
+    rot_prefix[i] = (int32_t)rot;
     lphase[i] = l.phase;
     pblocks[l.phase] += L.blocks;
+    for (int b = 0; b < L.blocks; ++b) sched_o[total + b] = (i << kStackBlockBits) | b;
     total += L.blocks;
+    if (z.zbuf_bytes) {
+      rot += batch * rot_tiles((int)g.G4);
+      zoff += zbuf_linear_bytes(batch, g.G4);
+    }
   }
-  if (st == TP_OK && total > INT32_MAX) st = TP_ERR_BAD_DIMS;
   if (st == TP_OK) {
     prefix[n_linears] = (int32_t)total;
+    rot_prefix[n_linears] = (int32_t)rot;
+    // Unordered schedule: blocks of the longest K first (stable), so the
+    // launch ends on short blocks.
+    std::vector<int> order(n_linears);
+    for (int i = 0; i < n_linears; ++i) order[i] = i;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int b) { return lin[a].G4 > lin[b].G4; });
+    int64_t k = 0;
+    for (int i : order)
+      for (int b = 0; b < lin[i].blocks; ++b) sched_u[k++] = (i << kStackBlockBits) | b;
     h->n_lin = n_linears;
     h->total_blocks = (int32_t)total;
-    h->n_phases = n_phases;
+    h->n_phases = z.n_phases;
     h->batch = (int32_t)batch;
-    h->pdone_offset = (int64_t)o_pdone;
-    if (hipMemcpy(plan, host, need, hipMemcpyHostToDevice) != hipSuccess) st = TP_ERR_HIP;
+    h->n_rot = (int32_t)rot;
+    h->min_g4 = (int32_t)z.min_g4;
+    h->zbuf_bytes = z.zbuf_bytes;
+    if (hipMemcpy(plan, host, lay.zbuf, hipMemcpyHostToDevice) != hipSuccess) st = TP_ERR_HIP;
   }
   free(host);
   return st;
+}
+
+extern "C" int tp_stack_rotate(void* plan, int64_t batch, void* stream) {
+  if (!plan) return TP_ERR_NULL_POINTER;
+  if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
+  if (batch > kSlotMaxBatch) return TP_OK;  // the LDS kernel rotates on the fly
+  const char* ro = reinterpret_cast<const char*>(plan) + kStackRO;
+  hipLaunchKernelGGL(tcq_stack_rotate_kernel, dim3(2 * device_cu_count()), dim3(kRotThreads), 0,
+                     (hipStream_t)stream, ro);
+  return launch_status();
+}
+
+extern "C" int tp_stack_gemv(void* plan, int64_t batch, const uint16_t* codebook, int bits,
+                             int n_states, int ordered, int64_t total_blocks, void* stream) {
+  if (!plan || !codebook) return TP_ERR_NULL_POINTER;
+  if (total_blocks < 1 || total_blocks > INT32_MAX) return TP_ERR_BAD_DIMS;
+  if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
+  const int spin_limit = 1 << 22;  // ~ seconds of s_sleep polling; ends the wait regardless
+  char* p = reinterpret_cast<char*>(plan);
+  hipStream_t s = (hipStream_t)stream;
+  switch (bits * 100 + n_states) {
+    case 204: return launch_gemv<2, 4>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    case 208: return launch_gemv<2, 8>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    case 216: return launch_gemv<2, 16>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    case 264: return launch_gemv<2, 64>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    case 304: return launch_gemv<3, 4>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    case 308: return launch_gemv<3, 8>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    case 316: return launch_gemv<3, 16>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    case 364: return launch_gemv<3, 64>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    default: return TP_ERR_UNSUPPORTED_STATES;
+  }
 }
 
 extern "C" int tp_stack_run(void* plan, int64_t batch, const uint16_t* codebook, int bits,
                             int n_states, int ordered, int64_t total_blocks, void* stream) {
   if (!plan || !codebook) return TP_ERR_NULL_POINTER;
   if (total_blocks < 1 || total_blocks > INT32_MAX) return TP_ERR_BAD_DIMS;
-  if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
-  const int nbt = batch <= 16 ? 1 : 2;
-  const int cus = device_cu_count();
-  const int per_cu = batch <= 8 ? 2 : 1;
-  const int grid = (int)(total_blocks < (int64_t)cus * per_cu ? total_blocks : (int64_t)cus * per_cu);
-  const int spin_limit = 1 << 22;  // ~ seconds of s_sleep polling; ends the wait regardless
-  char* p = reinterpret_cast<char*>(plan);
-  hipStream_t s = (hipStream_t)stream;
-#define TP_STACK(KB, NS)                                                       \
-  (nbt == 1 ? launch_stack<KB, NS, 1>(p, grid, batch, codebook, ordered, spin_limit, s) \
-            : launch_stack<KB, NS, 2>(p, grid, batch, codebook, ordered, spin_limit, s))
-  switch (bits * 100 + n_states) {
-    case 204: TP_STACK(2, 4); break;
-    case 208: TP_STACK(2, 8); break;
-    case 216: TP_STACK(2, 16); break;
-    case 264: TP_STACK(2, 64); break;
-    case 304: TP_STACK(3, 4); break;
-    case 308: TP_STACK(3, 8); break;
-    case 316: TP_STACK(3, 16); break;
-    case 364: TP_STACK(3, 64); break;
-    default: return TP_ERR_UNSUPPORTED_STATES;
-  }
-#undef TP_STACK
-  return launch_status();
+  if (bits * 100 + n_states != 204 && bits * 100 + n_states != 208 && bits * 100 + n_states != 216 &&
+      bits * 100 + n_states != 264 && bits * 100 + n_states != 304 && bits * 100 + n_states != 308 &&
+      bits * 100 + n_states != 316 && bits * 100 + n_states != 364)
+    return TP_ERR_UNSUPPORTED_STATES;
+  const int st = tp_stack_rotate(plan, batch, stream);
+  if (st) return st;
+  return tp_stack_gemv(plan, batch, codebook, bits, n_states, ordered, total_blocks, stream);
 }
 
 extern "C" int64_t tp_stack_plan_blocks(const int64_t* ns, int n_linears) {

@@ -10,7 +10,8 @@
 //        X_x bit 2j+1 = path bit of column 64g + 32 + 16x + j   (second half)
 //   * member words [T][G][16 rows][MW]:
 //        k=3: M[x][h] (x = 0,1; h = first/second half), bits 2j..2j+1 = member
-//             of column 64g + 32h + 16x + j (the reference's own bit order);
+//             of column 64g + 32h + 16x + j (the reference's own bit order),
+//             then the two nibbles of every byte swapped;
 //        k=2: W[x], bits 4p..4p+1 = members of columns 64g + 16x + 2p, +1 and
 //             bits 4p+2..4p+3 = members of columns 64g + 32 + 16x + 2p, +1;
 //        k=4: the k=3 words of the low two member bits, then the k=2 words of
@@ -21,10 +22,11 @@
 // window with the trellis generators, i.e. XORs of the path stream delayed by
 // each generator tap.  On the interleaved word a delay of t columns is a left
 // funnel shift by 2t bits across (current word, previous word), so both
-// subset bits of 32 weights cost ~13 ALU ops.  Two weights' (subset, member)
-// bits form one byte that indexes a 256-entry table of fp16 pairs
-// (cb[level_a], cb[level_b]); the table is replicated 64x in LDS so every lane
-// reads its own bank (no conflicts).  The pairs feed
+// subset bits of 32 weights cost ~12 ALU ops.  Two weights' (subset, member)
+// bits form one byte (one bit-select per four bytes) that indexes a
+// 256-entry table of fp16 pairs (cb[level_a], cb[level_b]); the table is
+// replicated in LDS (k=3: two index formats x 32 lane copies, k=2: 64
+// copies) so the lanes of a half-wave read distinct banks.  The pairs feed
 // v_mfma_f32_16x16x32_f16 (rows x K) against the rotated activations (K x batch).
 // The row scale is applied once at the end (turbopress/triton_kernel.py:70-73,123).
 #include "tp_tiled_common.h"
@@ -58,7 +60,7 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
   const int wave = tid >> 6;
   const int r = lane & 15;   // A row / B,D column (batch)
   const int q = lane >> 4;   // K block of A and B, row block of D
-  const uint32_t laneoff = (uint32_t)lane << 2;
+  const uint32_t laneoff = lane_offsets<KB>(lane);
   const int batch = a.batch;
   bool table_ready = false;
   const uint32_t cb_lane = a.codebook[lane & ((2 << KB) - 1)];
@@ -221,7 +223,7 @@ tiled_decode_kernel(const uint32_t* __restrict__ path, const uint32_t* __restric
   __syncthreads();
   const int lane = threadIdx.x & 63;
   const int r = lane & 15, q = lane >> 4;
-  const uint32_t laneoff = (uint32_t)lane << 2;
+  const uint32_t laneoff = lane_offsets<KB>(lane);
   const int64_t unit = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (unit >= (int64_t)T * G4) return;
   const int t = (int)(unit / G4), gu = (int)(unit % G4);
@@ -274,6 +276,10 @@ __device__ __forceinline__ uint32_t pair_interleave16(uint32_t a, uint32_t b) {
   return o;
 }
 
+__device__ __forceinline__ uint32_t nibble_swap(uint32_t v) {
+  return ((v & 0x0F0F0F0Fu) << 4) | ((v >> 4) & 0x0F0F0F0Fu);
+}
+
 __global__ void retile_kernel(const uint8_t* __restrict__ path, int64_t ps,
                               const uint8_t* __restrict__ member, int64_t ms,
                               int64_t n, int64_t d, int bits, int64_t T, int64_t G,
@@ -310,9 +316,12 @@ __global__ void retile_kernel(const uint8_t* __restrict__ path, int64_t ps,
   out_path[idx * 2 + 1] = interleave16(h[0] >> 16, h[1] >> 16);
   const int mw = member_words(bits);
   uint32_t* mo = out_member + idx * mw;
-  // column groups: 0 = first half x=0, 1 = first half x=1, 2 = second half x=0, 3 = second half x=1
+  // column groups: 0 = first half x=0, 1 = first half x=1, 2 = second half x=0, 3 = second half x=1;
+  // 2-bit member words are stored with the two nibbles of every byte swapped
+  // (the decoder's index formation pairs them with subset nibbles in one op)
   if (bits == 3 || bits == 4) {
-    mo[0] = mlo[0]; mo[1] = mlo[2]; mo[2] = mlo[1]; mo[3] = mlo[3];
+    mo[0] = nibble_swap(mlo[0]); mo[1] = nibble_swap(mlo[2]);
+    mo[2] = nibble_swap(mlo[1]); mo[3] = nibble_swap(mlo[3]);
   }
   if (bits == 2) {
     mo[0] = pair_interleave16(m1[0], m1[2]);

@@ -69,21 +69,50 @@ __device__ __forceinline__ void subset_words(uint32_t cur, uint32_t prev, uint32
   constexpr int m = TrellisOf<NS>::m;
   constexpr uint32_t D0 = delay_mask(TrellisOf<NS>::g0, m);
   constexpr uint32_t D1 = delay_mask(TrellisOf<NS>::g1, m);
-  uint32_t e0 = (D0 & 1u) ? cur : 0u;
-  uint32_t e1 = (D1 & 1u) ? cur : 0u;
+  uint32_t sh[m + 1];
+  sh[0] = cur;
 #pragma unroll
-  for (int t = 1; t <= m; ++t) {
-    const uint32_t a = __builtin_amdgcn_alignbit(cur, prev, 32 - 2 * t);
-    if ((D0 >> t) & 1u) e0 ^= a;
-    if ((D1 >> t) & 1u) e1 ^= a;
+  for (int t = 1; t <= m; ++t) sh[t] = __builtin_amdgcn_alignbit(cur, prev, 32 - 2 * t);
+  uint32_t e0, e1;
+  if constexpr (NS == 64) {
+    // taps {0,1,2,4,5} and {0,1,4,5,6}: shared part first, three-input XORs
+    static_assert(D0 == 0x37u && D1 == 0x73u, "S=64 generator taps");
+    const uint32_t c = __builtin_amdgcn_bitop3_b32(sh[0], sh[1], sh[4], 0x96);
+    e0 = __builtin_amdgcn_bitop3_b32(c, sh[5], sh[2], 0x96);
+    e1 = __builtin_amdgcn_bitop3_b32(c, sh[5], sh[6], 0x96);
+  } else {
+    e0 = 0u;
+    e1 = 0u;
+#pragma unroll
+    for (int t = 0; t <= m; ++t) {
+      if ((D0 >> t) & 1u) e0 ^= sh[t];
+      if ((D1 >> t) & 1u) e1 ^= sh[t];
+    }
   }
   SA = (e0 & 0x55555555u) | ((e1 << 1) & 0xAAAAAAAAu);
   SB = ((e0 >> 1) & 0x55555555u) | (e1 & 0xAAAAAAAAu);
 }
 
-// LDS byte address of the lane's copy of table entry `byte b of idx`.
+// LDS byte address of the lane's copy of table entry `byte b of idx` in
+// table format f: (idx byte b) * 256 + byte f of laneoff.
+template <int F = 0>
 __device__ __forceinline__ uint32_t table_addr(uint32_t idx, uint32_t laneoff, int b) {
-  return __builtin_amdgcn_perm(idx, laneoff, 0x0C0C0000u | ((4u + b) << 8));
+  return __builtin_amdgcn_perm(idx, laneoff, 0x0C0C0000u | ((4u + b) << 8) | (uint32_t)F);
+}
+
+// Lane offsets inside a 256-byte table row.  k=2: one format, 64 lane
+// copies (byte 0 = lane * 4).  k=3: two formats of 32 copies each -- format
+// 0 (subset nibble low, member nibble high) at bytes 0..127, format 1
+// (member nibble low, subset nibble high) at 128..255 -- byte 0 / byte 1 of
+// the returned word.
+template <int KB>
+__device__ __forceinline__ uint32_t lane_offsets(int lane) {
+  if constexpr (KB == 3) {
+    const uint32_t c = (uint32_t)(lane & 31) << 2;
+    return c | ((128u + c) << 8);
+  } else {
+    return (uint32_t)lane << 2;
+  }
 }
 
 __device__ __forceinline__ uint32_t lds_word(const uint32_t* table, uint32_t byte_addr) {
@@ -103,11 +132,16 @@ __device__ __forceinline__ void decode_word(uint32_t cur, uint32_t prev, const M
   uint32_t SA, SB;
   subset_words<NS>(cur, prev, SA, SB);
   uint32_t iae, iao, ibe, ibo;
+  constexpr int FO = KB == 3 ? 1 : 0;  // table format of the odd-pair index words
   if constexpr (KB == 3) {
-    iae = (SA & 0x0F0F0F0Fu) | ((M.a << 4) & 0xF0F0F0F0u);
-    iao = ((SA >> 4) & 0x0F0F0F0Fu) | (M.a & 0xF0F0F0F0u);
-    ibe = (SB & 0x0F0F0F0Fu) | ((M.b << 4) & 0xF0F0F0F0u);
-    ibo = ((SB >> 4) & 0x0F0F0F0Fu) | (M.b & 0xF0F0F0F0u);
+    // Member words are stored nibble-swapped within each byte, so one bit
+    // select pairs every subset nibble with its member nibble: even pairs as
+    // [subset | member << 4] (format 0), odd pairs as [member | subset << 4]
+    // (format 1).
+    iae = (SA & 0x0F0F0F0Fu) | (M.a & 0xF0F0F0F0u);
+    iao = (SA & 0xF0F0F0F0u) | (M.a & 0x0F0F0F0Fu);
+    ibe = (SB & 0x0F0F0F0Fu) | (M.b & 0xF0F0F0F0u);
+    ibo = (SB & 0xF0F0F0F0u) | (M.b & 0x0F0F0F0Fu);
   } else {
     iae = (SA & 0x0F0F0F0Fu) | ((M.w << 4) & 0xF0F0F0F0u);
     iao = ((SA >> 4) & 0x0F0F0F0Fu) | (M.w & 0xF0F0F0F0u);
@@ -116,39 +150,49 @@ __device__ __forceinline__ void decode_word(uint32_t cur, uint32_t prev, const M
   }
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    A[0][2 * h] = lds_word(table, table_addr(iae, laneoff, h));
-    A[0][2 * h + 1] = lds_word(table, table_addr(iao, laneoff, h));
-    A[1][2 * h] = lds_word(table, table_addr(iae, laneoff, 2 + h));
-    A[1][2 * h + 1] = lds_word(table, table_addr(iao, laneoff, 2 + h));
-    A[2][2 * h] = lds_word(table, table_addr(ibe, laneoff, h));
-    A[2][2 * h + 1] = lds_word(table, table_addr(ibo, laneoff, h));
-    A[3][2 * h] = lds_word(table, table_addr(ibe, laneoff, 2 + h));
-    A[3][2 * h + 1] = lds_word(table, table_addr(ibo, laneoff, 2 + h));
+    A[0][2 * h] = lds_word(table, table_addr<0>(iae, laneoff, h));
+    A[0][2 * h + 1] = lds_word(table, table_addr<FO>(iao, laneoff, h));
+    A[1][2 * h] = lds_word(table, table_addr<0>(iae, laneoff, 2 + h));
+    A[1][2 * h + 1] = lds_word(table, table_addr<FO>(iao, laneoff, 2 + h));
+    A[2][2 * h] = lds_word(table, table_addr<0>(ibe, laneoff, h));
+    A[2][2 * h + 1] = lds_word(table, table_addr<FO>(ibo, laneoff, h));
+    A[3][2 * h] = lds_word(table, table_addr<0>(ibe, laneoff, 2 + h));
+    A[3][2 * h + 1] = lds_word(table, table_addr<FO>(ibo, laneoff, 2 + h));
   }
 }
 
-// Pair table: entry v = (cb[level_a] | cb[level_b] << 16), with the index byte
-// v = [S0a S1a S0b S1b | member bits], replicated in 64 lane copies.
+// Pair table: 256 rows of 256 bytes; row v holds entry (cb[level_a] |
+// cb[level_b] << 16) of index byte v in lane copies.  k=2: index byte v =
+// [S0a S1a S0b S1b | Ma Mb ..], 64 copies.  k=3: format 0 (bytes 0..127, 32
+// copies) reads v = [S0a S1a S0b S1b | M0a M1a M0b M1b], format 1 (bytes
+// 128..255, 32 copies) the same fields with the nibbles swapped.
 template <int KB>
-__device__ __forceinline__ uint32_t pair_entry(const uint16_t* cb, uint32_t v) {
-  const uint32_t sa = v & 3u, sb = (v >> 2) & 3u;
-  uint32_t ma, mb;
+__device__ __forceinline__ void pair_fields(uint32_t v, int fmt, uint32_t& sa, uint32_t& sb, uint32_t& ma,
+                                            uint32_t& mb) {
   if constexpr (KB == 3) {
-    ma = (v >> 4) & 3u;
-    mb = (v >> 6) & 3u;
+    const uint32_t s = fmt ? v >> 4 : v, m = fmt ? v : v >> 4;
+    sa = s & 3u;
+    sb = (s >> 2) & 3u;
+    ma = m & 3u;
+    mb = (m >> 2) & 3u;
   } else {
+    (void)fmt;
+    sa = v & 3u;
+    sb = (v >> 2) & 3u;
     ma = (v >> 4) & 1u;
     mb = (v >> 5) & 1u;
   }
-  return (uint32_t)cb[ma * 4 + sa] | ((uint32_t)cb[mb * 4 + sb] << 16);
 }
 
 template <int KB>
 __device__ void build_pair_table(uint32_t* table, const uint16_t* cb, int tid, int nthreads) {
-  // Each thread writes 16-byte runs (4 lane copies) of one entry.
+  // Each thread writes 16-byte runs (4 lane copies) of one entry: 16 runs
+  // per row, runs 8..15 are format 1 for k=3.
   for (int i = tid; i < kTableWords / 4; i += nthreads) {
-    const uint32_t v = (uint32_t)(i >> 4);  // 16 runs of 4 copies per entry
-    const uint32_t e = pair_entry<KB>(cb, v);
+    const uint32_t v = (uint32_t)(i >> 4);
+    uint32_t sa, sb, ma, mb;
+    pair_fields<KB>(v, (i & 15) >= 8, sa, sb, ma, mb);
+    const uint32_t e = (uint32_t)cb[ma * 4 + sa] | ((uint32_t)cb[mb * 4 + sb] << 16);
     u32x4_t run = {e, e, e, e};
     *reinterpret_cast<u32x4_t*>(table + 4 * i) = run;
   }
@@ -160,15 +204,8 @@ template <int KB>
 __device__ void build_pair_table_lanes(uint32_t* table, uint32_t cb_lane, int tid, int nthreads) {
   for (int i = tid; i < kTableWords / 4; i += nthreads) {
     const uint32_t v = (uint32_t)(i >> 4);
-    const uint32_t sa = v & 3u, sb = (v >> 2) & 3u;
-    uint32_t ma, mb;
-    if constexpr (KB == 3) {
-      ma = (v >> 4) & 3u;
-      mb = (v >> 6) & 3u;
-    } else {
-      ma = (v >> 4) & 1u;
-      mb = (v >> 5) & 1u;
-    }
+    uint32_t sa, sb, ma, mb;
+    pair_fields<KB>(v, (i & 15) >= 8, sa, sb, ma, mb);
     const uint32_t lo = (uint32_t)__shfl((int)cb_lane, (int)(ma * 4 + sa), 64);
     const uint32_t hi = (uint32_t)__shfl((int)cb_lane, (int)(mb * 4 + sb), 64);
     const uint32_t e = (lo & 0xFFFFu) | (hi << 16);
@@ -198,6 +235,7 @@ struct LinearDesc {
   uint16_t* y;             // fp16 [batch][ldy]
   float* ws;               // [T*16][16*NBT] fp32 split-K sums (kept zero between calls)
   uint32_t* cnt;           // [T] split-K unit counters (kept zero between calls)
+  uint16_t* z;             // stack plans: rotated activations fp16 [batch][G4 * 256]
   float hdiv;              // fp32(sqrt(hb))
   int32_t n, d, T, G, G4;
   int32_t ldx, ldy, kg, blocks;  // kg: units per block; blocks: ceil(T/8)*ceil(G4/kg)

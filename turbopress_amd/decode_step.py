@@ -71,7 +71,7 @@ class LinearStack:
                 self.outputs[i].data_ptr(), lin.out_features, lin.out_features, lin.in_features, ph, 0)
         self.n_phases = max(self.phases) + 1
         lib = _lib.lib()
-        nbytes = int(lib.tp_stack_plan_bytes(len(lins), self.n_phases))
+        nbytes = int(lib.tp_stack_plan_bytes(arr, len(lins), l0.bits, self.batch))
         if nbytes <= 0:
             raise ValueError("invalid stack size")
         self.plan = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
@@ -90,6 +90,20 @@ class LinearStack:
                                      self.bits, self.n_states, int(self.ordered), self.total_blocks,
                                      hk.current_stream_ptr(self.plan.device))
         _lib.check(st, "stack_run")
+        return self.outputs
+
+    def rotate(self) -> None:
+        """First launch of run(): rotate every input into the plan's z buffer."""
+        _lib.check(_lib.lib().tp_stack_rotate(self.plan.data_ptr(), self.batch,
+                                              hk.current_stream_ptr(self.plan.device)), "stack_rotate")
+
+    def gemv(self) -> list:
+        """Second launch of run(): every GEMV, from the z buffer the last
+        rotate() filled (batch <= 8) or from the inputs (batch > 8)."""
+        st = _lib.lib().tp_stack_gemv(self.plan.data_ptr(), self.batch, self.codebook.data_ptr(),
+                                      self.bits, self.n_states, int(self.ordered), self.total_blocks,
+                                      hk.current_stream_ptr(self.plan.device))
+        _lib.check(st, "stack_gemv")
         return self.outputs
 
     def error(self) -> int:
