@@ -36,6 +36,7 @@ import json
 import os
 import sys
 import time
+from pathlib import Path
 
 import torch
 
@@ -130,6 +131,43 @@ def time_gemv_kernel(stack, steps, warmup):
     return start.elapsed_time(end) / steps * 1e3
 
 
+TRAFFIC_PROFILE = Path(__file__).resolve().parent / "profiles" / "tcq_stack_slot_kernel_qwen3-4b_b1_hbm_traffic.md"
+
+
+def measured_traffic():
+    """HBM bytes per GEMV launch from the committed counter summary (FETCH_SIZE
+    and WRITE_SIZE passes calibrated against a known-size copy), or None."""
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def copy_reference(mib: int, reps: int = 10):
+    """A plain device-to-device copy of `mib` MiB (read + write), timed like
+    the GEMV: the practical streaming bandwidth of this box, and the known-size
+    kernel that HBM byte counters are calibrated against."""
+    a = torch.ones(mib << 18, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        b.copy_(a)
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) / reps * 1e3
+    moved = 2 * a.numel() * 4
+    del a, b
+    return {"bytes_read": moved // 2, "bytes_written": moved // 2, "us": round(us, 2),
+            "gbps": round(moved / (us * 1e-6) / 1e9, 1)}
+
+
 def cpu_baseline(budget_s: float):
     """The reference's CPU tiled path (oracle restatement), one Qwen3-4B layer
     at k=3, B=1, repeated until ~budget_s of CPU work, scaled to 36 layers."""
@@ -171,6 +209,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=300)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--copy-mib", type=int, default=1024,
+                    help="size of the device copy reported as copy_reference (0: skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-primary", action="store_true", help="skip the comparison executors")
     args = ap.parse_args()
@@ -220,6 +260,9 @@ def main() -> int:
         extra = {"phase_ordered_stack_us": round(ms_o * 1e3, 2), "grouped_launches_us": round(ms_g * 1e3, 2),
                  "per_linear_launches_us": round(ms_p * 1e3, 2)}
 
+    copy_ref = copy_reference(args.copy_mib) if args.copy_mib > 0 else None
+    if copy_ref:
+        log(f"device copy {args.copy_mib} MiB: {copy_ref['gbps']} GB/s (read + write)")
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline")
@@ -239,11 +282,12 @@ def main() -> int:
                    "bytes_per_step": nbytes},
         "gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
         "wall_ms_per_step": round(ms_wall, 5),
-        "roofline": {"kernel": "tcq_stack_slot_kernel<3,64,2> (all 252 linears, one launch per step)",
+        "roofline": {"kernel": "tcq_stack_slot_kernel<3,64,4> (all 252 linears, one launch per step)",
                      "bound": "hbm", "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
                      "us_per_launch": round(us_gemv, 2), "bytes_per_launch": gemv_bytes},
         "executors": extra,
+        "copy_reference": copy_ref,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
