@@ -79,3 +79,30 @@ def test_check_maps_status_to_reference_exceptions():
     with pytest.raises(RuntimeError):
         _lib.check(_lib.TP_ERR_HIP, "x")
     _lib.check(_lib.TP_OK, "x")
+
+
+def test_device_code_indexes_no_register_arrays(tmp_path):
+    """Every loop over a register array unrolls to constant indices: the
+    device code holds no VGPR-indexed moves.  (A loop the compiler cannot
+    unroll turns v[e + h] into indexed moves, and once if-converted those
+    write past the array into unrelated live registers.)"""
+    import shutil
+    import subprocess
+    from concurrent.futures import ThreadPoolExecutor
+    from turbopress_amd import build as B
+    if not Path(B.HIPCC).exists() and shutil.which(B.HIPCC) is None:
+        pytest.skip("hipcc not available")
+
+    def compile_asm(src):
+        out = tmp_path / (src.stem + ".s")
+        res = subprocess.run([B.HIPCC, *B.HIP_FLAGS, f"-I{B.CSRC}", "--cuda-device-only", "-S", str(src),
+                              "-o", str(out)], capture_output=True, text=True)
+        assert res.returncode == 0, res.stderr[-2000:]
+        return src.name, out.read_text(), res.stderr
+
+    with ThreadPoolExecutor(max_workers=4) as ex:
+        results = list(ex.map(compile_asm, sorted(B.CSRC.glob("*.hip"))))
+    for name, asm, log in results:
+        assert "loop not unrolled" not in log, name
+        for insn in ("s_set_gpr_idx_on", "v_movrels", "v_movreld", "v_movrelsd"):
+            assert insn not in asm, (name, insn)

@@ -240,26 +240,31 @@ tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
       }
     }
     const int hmax = hb < kRotTile ? hb : kRotTile;
+    // Stages are skipped with a (uniform) condition, never a loop exit: the
+    // loops must unroll so that every v[] index is a compile-time constant (a
+    // runtime stage distance would index the register array dynamically).
 #pragma unroll
     for (int h = 1; h < kRotEPT; h <<= 1) {
-      if (h >= hmax) break;
+      if (h < hmax) {
 #pragma unroll
-      for (int e = 0; e < kRotEPT; ++e) {
-        if ((e & h) == 0) {
-          const float a = v[e], c = v[e + h];
-          v[e] = a + c;
-          v[e + h] = a - c;
+        for (int e = 0; e < kRotEPT; ++e) {
+          if ((e & h) == 0) {
+            const float a = v[e], c = v[e + h];
+            v[e] = a + c;
+            v[e + h] = a - c;
+          }
         }
       }
     }
 #pragma unroll
     for (int sft = 0; sft < 6; ++sft) {
-      if ((kRotEPT << sft) >= hmax) break;
-      const bool upper = (lane >> sft) & 1;
+      if ((kRotEPT << sft) < hmax) {
+        const bool upper = (lane >> sft) & 1;
 #pragma unroll
-      for (int e = 0; e < kRotEPT; ++e) {
-        const float p = __shfl_xor(v[e], 1 << sft, 64);
-        v[e] = upper ? p - v[e] : v[e] + p;
+        for (int e = 0; e < kRotEPT; ++e) {
+          const float p = __shfl_xor(v[e], 1 << sft, 64);
+          v[e] = upper ? p - v[e] : v[e] + p;
+        }
       }
     }
     if (hmax > 1024) {  // distances 1024 (and 2048): wave bits of the column
