@@ -75,7 +75,7 @@ struct StackInfo {
 };
 
 struct StackLayout {
-  size_t lin, prefix, lphase, pblocks, sched_o, sched_u, rot_prefix, pdone, zbuf, total;
+  size_t lin, prefix, lphase, pblocks, sched_o, sched_u, rot_prefix, rot_lin, pdone, zbuf, total;
 };
 
 constexpr size_t kStackRO = sizeof(StackCounters);
@@ -90,7 +90,7 @@ __device__ __forceinline__ const TP_CONST T& cread(const T* p) {
   return *(const TP_CONST T*)p;
 }
 
-__host__ __device__ inline StackLayout stack_layout(int n_lin, int n_phases, int total_blocks,
+__host__ __device__ inline StackLayout stack_layout(int n_lin, int n_phases, int total_blocks, int n_rot,
                                                     int64_t zbuf_bytes) {
   StackLayout p;
   size_t o = kStackRO + sizeof(StackInfo);
@@ -108,6 +108,8 @@ __host__ __device__ inline StackLayout stack_layout(int n_lin, int n_phases, int
   o += sizeof(int32_t) * (size_t)total_blocks;
   p.rot_prefix = o;
   o += sizeof(int32_t) * (size_t)(n_lin + 1);
+  p.rot_lin = o;
+  o += sizeof(int32_t) * (size_t)n_rot;
   o = (o + 63) & ~(size_t)63;
   p.pdone = o;
   o += sizeof(uint32_t) * (size_t)n_phases;
@@ -126,7 +128,8 @@ struct StackRO {  // views into the read-only part
   const int32_t* pblocks;  // [n_phases] blocks per phase
   const int32_t* sched_o;  // [total] (linear << 20) | block, phase order
   const int32_t* sched_u;  // [total] same blocks, longest K first
-  const int32_t* rot_prefix;
+  const int32_t* rot_prefix;  // [n_lin + 1] first rotation item of each linear
+  const int32_t* rot_lin;     // [n_rot] linear of each rotation item
   size_t pdone;            // byte offset of pdone from the plan start
   size_t zbuf;             // byte offset of the z buffer from the plan start
 };
@@ -135,7 +138,7 @@ struct StackRO {  // views into the read-only part
 __device__ inline StackRO stack_ro(const char* __restrict__ ro) {
   const StackInfo* info = reinterpret_cast<const StackInfo*>(ro);
   const TP_CONST StackInfo& ci = cread(info);
-  const StackLayout l = stack_layout(ci.n_lin, ci.n_phases, ci.total_blocks, ci.zbuf_bytes);
+  const StackLayout l = stack_layout(ci.n_lin, ci.n_phases, ci.total_blocks, ci.n_rot, ci.zbuf_bytes);
   StackRO v;
   v.info = info;
   v.lin = reinterpret_cast<const LinearDesc*>(ro + (l.lin - kStackRO));
@@ -145,6 +148,7 @@ __device__ inline StackRO stack_ro(const char* __restrict__ ro) {
   v.sched_o = reinterpret_cast<const int32_t*>(ro + (l.sched_o - kStackRO));
   v.sched_u = reinterpret_cast<const int32_t*>(ro + (l.sched_u - kStackRO));
   v.rot_prefix = reinterpret_cast<const int32_t*>(ro + (l.rot_prefix - kStackRO));
+  v.rot_lin = reinterpret_cast<const int32_t*>(ro + (l.rot_lin - kStackRO));
   v.pdone = l.pdone;
   v.zbuf = l.zbuf;
   return v;
@@ -182,11 +186,31 @@ constexpr int kRotEPT = kRotTile / kRotThreads;  // 16
 
 __host__ __device__ inline int rot_tiles(int G4) { return (G4 * kChunkCols + kRotTile - 1) / kRotTile; }
 
-__device__ __forceinline__ void load16(const uint16_t* p, float v[kRotEPT], int valid_groups) {
+constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferFlags);
+}
+
+// 16 halves at byte offset `off` of a buffer, as fp32.  The four 8-byte
+// loads are issued together; groups past the buffer's end read as zeros
+// (every d is a multiple of 4, so a group is wholly inside or outside).
+// Each load gets its own opaque offset register so that the compiler does
+// not merge two of them into one 16-byte access, which could straddle the
+// end of the buffer.
+__device__ __forceinline__ void load16(__amdgpu_buffer_rsrc_t r, uint32_t off, float v[kRotEPT]) {
+  u32x2_t w[kRotEPT / 4];
 #pragma unroll
   for (int g = 0; g < kRotEPT / 4; ++g) {
-    float t[4] = {0.f, 0.f, 0.f, 0.f};
-    if (g < valid_groups) unpack4h(gld2(p + 4 * g), t);
+    uint32_t o = off + 8u * g;
+    __asm__("" : "+v"(o));
+    w[g] = __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0);
+  }
+#pragma unroll
+  for (int g = 0; g < kRotEPT / 4; ++g) {
+    float t[4];
+    unpack4h(make_uint2(w[g][0], w[g][1]), t);
 #pragma unroll
     for (int e = 0; e < 4; ++e) v[4 * g + e] = t[e];
   }
@@ -196,32 +220,26 @@ __global__ void __launch_bounds__(kRotThreads)
 tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
   __shared__ float ex[kRotTile];
   const StackRO P = stack_ro(plan_ro);
-  const int n_rot = P.info->n_rot;
-  const int n_lin = P.info->n_lin;
+  const int n_rot = cread(P.info).n_rot;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   for (int item = blockIdx.x; item < n_rot; item += gridDim.x) {
-    int lo = 0, hi = n_lin - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (P.rot_prefix[mid] <= item) lo = mid; else hi = mid - 1;
-    }
-    const int li = __builtin_amdgcn_readfirstlane(lo);
-    const LinearDesc L = P.lin[li];
+    // plan lookups are scalar loads: one dependent load per level
+    const int li = cread(P.rot_lin + item);
+    const TP_CONST LinearDesc& L = cread(P.lin + li);
     const int ntiles = rot_tiles(L.G4);
-    const int local = item - P.rot_prefix[li];
+    const int local = item - cread(P.rot_prefix + li);
     const int b = local / ntiles, k = local - b * ntiles;
     const int c0 = k * kRotTile + tid * kRotEPT;      // first column of this thread
     const int hb = L.hb;
-    const uint16_t* xr = L.x + (size_t)b * L.ldx;
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(L.x + (size_t)b * L.ldx, (uint32_t)L.d * 2u);
+    const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(L.rs, (uint32_t)L.d * 2u);
     float v[kRotEPT];
     if (hb <= kRotTile) {
-      // d is a multiple of 4: 4-column groups are wholly inside or outside.
-      const int groups = max(0, min(kRotEPT / 4, (L.d - c0) / 4));
       float rv[kRotEPT];
-      load16(xr + c0, v, groups);
-      load16(L.rs + c0, rv, groups);
+      load16(xrs, (uint32_t)c0 * 2u, v);
+      load16(rrs, (uint32_t)c0 * 2u, rv);
 #pragma unroll
       for (int e = 0; e < kRotEPT; ++e) v[e] *= rv[e];
     } else {
@@ -232,8 +250,8 @@ tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
       for (int i = 0; i < hb / kRotTile; ++i) {
         const int c = base + i * kRotTile + tid * kRotEPT;
         float xv[kRotEPT], rv[kRotEPT];
-        load16(xr + c, xv, kRotEPT / 4);
-        load16(L.rs + c, rv, kRotEPT / 4);
+        load16(xrs, (uint32_t)c * 2u, xv);
+        load16(rrs, (uint32_t)c * 2u, rv);
         const bool neg = __popc(i & o) & 1;
 #pragma unroll
         for (int e = 0; e < kRotEPT; ++e) v[e] += neg ? -(xv[e] * rv[e]) : xv[e] * rv[e];
@@ -306,12 +324,6 @@ tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
 // ---------------------------------------------------------------------------
 // 2. slot kernel (batch <= 8)
 // ---------------------------------------------------------------------------
-constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format
-constexpr uint32_t kOutOfRange = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferFlags);
-}
 
 __device__ __forceinline__ u32x2_t gld2v(const char* p) { return *(const TP_GLOBAL u32x2_t*)p; }
 
@@ -938,7 +950,7 @@ extern "C" int64_t tp_stack_plan_bytes(const tp_stack_linear* linears, int n_lin
   if (bits != 2 && bits != 3) return 0;
   StackSizes z;
   if (stack_sizes(linears, n_linears, bits, batch, &z) != TP_OK) return 0;
-  return (int64_t)stack_layout(n_linears, z.n_phases, (int)z.total_blocks, z.zbuf_bytes).total;
+  return (int64_t)stack_layout(n_linears, z.n_phases, (int)z.total_blocks, (int)z.n_rot, z.zbuf_bytes).total;
 }
 
 extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears, int bits,
@@ -948,7 +960,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
   StackSizes z;
   int st = stack_sizes(linears, n_linears, bits, batch, &z);
   if (st) return st;
-  const StackLayout lay = stack_layout(n_linears, z.n_phases, (int)z.total_blocks, z.zbuf_bytes);
+  const StackLayout lay = stack_layout(n_linears, z.n_phases, (int)z.total_blocks, (int)z.n_rot, z.zbuf_bytes);
   if (plan_bytes < (int64_t)lay.total) return TP_ERR_WORKSPACE;
   if ((uintptr_t)plan & 255) return TP_ERR_MISALIGNED;
   // Everything before the z buffer is written from the host; every run
@@ -963,6 +975,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
   int32_t* sched_o = reinterpret_cast<int32_t*>(host + lay.sched_o);
   int32_t* sched_u = reinterpret_cast<int32_t*>(host + lay.sched_u);
   int32_t* rot_prefix = reinterpret_cast<int32_t*>(host + lay.rot_prefix);
+  int32_t* rot_lin = reinterpret_cast<int32_t*>(host + lay.rot_lin);
   char* zbuf = reinterpret_cast<char*>(plan) + lay.zbuf;
   int64_t total = 0, rot = 0, zoff = 0;
   for (int i = 0; i < n_linears; ++i) {
@@ -1010,6 +1023,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     for (int b = 0; b < L.blocks; ++b) sched_o[total + b] = (i << kStackBlockBits) | b;
     total += L.blocks;
     if (z.zbuf_bytes) {
+      for (int64_t j = 0; j < batch * rot_tiles((int)g.G4); ++j) rot_lin[rot + j] = i;
       rot += batch * rot_tiles((int)g.G4);
       zoff += zbuf_linear_bytes(batch, z.zrow);
     }
