@@ -34,9 +34,7 @@
 #include "tp_tiled_common.h"
 
 #include <algorithm>
-#include <mutex>
 #include <type_traits>
-#include <unordered_map>
 #include <vector>
 
 namespace tp {
@@ -70,8 +68,6 @@ struct StackInfo {
   int32_t n_rot;          // rotation tiles (batch * 4096-column tiles per linear) when the plan has a z buffer
   int32_t min_g4;         // shortest K of the plan in 256-column units
   int64_t zbuf_bytes;
-  int32_t zrow;           // halves per z row, common to all linears (longest K, 256-aligned)
-  int32_t reserved;
 };
 
 struct StackLayout {
@@ -180,18 +176,19 @@ __device__ inline void wait_phase(const StackRO& P, uint32_t* pdone, StackCounte
 // sqrt(block)), all in fp32, z rounded to fp16 once.  A block larger than
 // 4096 (H_hb = H_(hb/4096) (x) H_4096) first sums its 4096-column sub-tiles
 // with the signs of the tile's row of H_(hb/4096).
-constexpr int kRotTile = 4096;
-constexpr int kRotThreads = 256;
-constexpr int kRotEPT = kRotTile / kRotThreads;  // 16
-
-__host__ __device__ inline int rot_tiles(int G4) { return (G4 * kChunkCols + kRotTile - 1) / kRotTile; }
-
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format
 constexpr uint32_t kOutOfRange = 0x80000000u;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferFlags);
 }
+
+constexpr int kRotTile = 4096;
+constexpr int kRotThreads = 256;
+constexpr int kRotEPT = kRotTile / kRotThreads;  // 16
+
+__host__ __device__ inline int rot_tiles(int G4) { return (G4 * kChunkCols + kRotTile - 1) / kRotTile; }
+
 
 // 16 halves at byte offset `off` of a buffer, as fp32.  The four 8-byte
 // loads are issued together; groups past the buffer's end read as zeros
@@ -310,7 +307,7 @@ tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
       }
     }
     const int zld = L.G4 * kChunkCols;               // columns written (zero past d)
-    uint16_t* zr = L.z + (size_t)b * cread(P.info).zrow;
+    uint16_t* zr = L.z + (size_t)b * zld;
 #pragma unroll
     for (int g = 0; g < kRotEPT / 4; ++g) {
       if (c0 + 4 * g >= zld) break;
@@ -430,57 +427,52 @@ __device__ __forceinline__ BlockInfo stream_info(const SlotEnv& E, int blk) {
   return b;
 }
 
-// Where the stream loads from (wave-uniform): buffer descriptors of one
-// block's tile of path/member words and the byte offset of the linear's z
-// rows in the z buffer.
+// Where the stream loads from: buffer descriptors of one block's tile of
+// path/member words, the linear's z rows and this lane's z offsets.
+template <int NZ>
 struct LoadCtx {
-  const char* path;     // path words of the wave's row tile
-  const char* member;   // member words of the wave's row tile
-  uint32_t zoff;
+  __amdgpu_buffer_rsrc_t prs, mrs;
+  uint32_t zoff;       // byte offset of the linear's z rows in the z buffer
+  uint32_t zv[NZ];     // lane offsets inside the z rows (per-lane)
   int G4;
 };
 
-template <int MW>
-__device__ __forceinline__ LoadCtx stream_ctx(const SlotEnv& E, const BlockInfo& b) {
+template <int MW, int SB, int NZ>
+__device__ __forceinline__ LoadCtx<NZ> stream_ctx(const SlotEnv& E, const BlockInfo& b) {
+  constexpr int SLOTS = 16 / SB;
   const TP_CONST LinearDesc& L = cread(E.P.lin + b.li);
   const int tt = b.t < L.T ? b.t : 0;
-  LoadCtx c;
-  c.path = reinterpret_cast<const char*>(L.path) + (size_t)tt * L.G * (kTileRows * 2 * 4);
-  c.member = reinterpret_cast<const char*>(L.member) + (size_t)tt * L.G * (kTileRows * MW * 4);
+  LoadCtx<NZ> c;
+  const uint32_t unit_p = 4u * kTileRows * 8u, unit_m = 4u * kTileRows * MW * 4u;
+  c.prs = buffer_rsrc(reinterpret_cast<const char*>(L.path) + (size_t)tt * L.G * (kTileRows * 2 * 4),
+                      (uint32_t)L.G4 * unit_p);
+  c.mrs = buffer_rsrc(reinterpret_cast<const char*>(L.member) + (size_t)tt * L.G * (kTileRows * MW * 4),
+                      (uint32_t)L.G4 * unit_m);
   c.zoff = (uint32_t)(reinterpret_cast<const char*>(L.z) - E.zbuf);
+  const uint32_t zld = (uint32_t)L.G4 * kChunkCols;
+#pragma unroll
+  for (int l = 0; l < NZ; ++l) {
+    const int i = l * SLOTS + E.slot;  // the MFMA whose B column this lane supplies
+    c.zv[l] = E.bb < E.batch ? ((uint32_t)E.bb * zld + (uint32_t)(E.q * kSegCols + mfma_col(i))) * 2u
+                             : kOutOfRange;  // out of range: zeros, no memory traffic
+  }
   c.G4 = b.G4;
   return c;
 }
 
-// This lane's z byte offsets inside any linear's z rows (rows share one
-// stride, so they do not depend on the block): load l feeds MFMA l*SLOTS +
-// slot; lanes past the batch read out of range (zeros, no memory traffic).
-template <int SB, int NZ>
-__device__ __forceinline__ void stream_zlane(const SlotEnv& E, int zrow, uint32_t zv[NZ]) {
-  constexpr int SLOTS = 16 / SB;
-#pragma unroll
-  for (int l = 0; l < NZ; ++l) {
-    const int i = l * SLOTS + E.slot;
-    zv[l] = E.bb < E.batch ? ((uint32_t)E.bb * (uint32_t)zrow + (uint32_t)(E.q * kSegCols + mfma_col(i))) * 2u
-                           : kOutOfRange;
-  }
-}
-
 template <int MW, int NZ>
-__device__ __forceinline__ UnitRegs<MW, NZ> stream_load(const SlotEnv& E, const char* path, const char* member,
-                                                        uint32_t zoff, const uint32_t* zv, int gu) {
+__device__ __forceinline__ UnitRegs<MW, NZ> stream_load(const SlotEnv& E, const LoadCtx<NZ>& c, int gu) {
   constexpr uint32_t unit_p = 4u * kTileRows * 8u;        // path bytes per unit
   constexpr uint32_t unit_m = 4u * kTileRows * MW * 4u;   // member bytes per unit
   constexpr uint32_t unit_z = kChunkCols * 2u;            // z bytes per unit and batch row
   UnitRegs<MW, NZ> g;
-  // scalar base + 32-bit lane offset: global loads in saddr form
-  const TP_GLOBAL char* pb = (const TP_GLOBAL char*)path + (uint32_t)gu * unit_p;
-  const TP_GLOBAL char* mb = (const TP_GLOBAL char*)member + (uint32_t)gu * unit_m;
-  g.X = *(const TP_GLOBAL u32x2_t*)(pb + E.pv);
-  g.M = *(const TP_GLOBAL typename MemberBuf<MW>::type*)(mb + E.mv);
+  g.X = __builtin_amdgcn_raw_buffer_load_b64(c.prs, E.pv, (uint32_t)gu * unit_p, 0);
+  g.M = MemberBuf<MW>::load(c.mrs, E.mv, (uint32_t)gu * unit_m);
+  // (uniform by construction; readfirstlane keeps it in a scalar register
+  // when the compiler merges it with per-lane values)
+  const uint32_t zs = (uint32_t)__builtin_amdgcn_readfirstlane((int)(c.zoff + (uint32_t)gu * unit_z));
 #pragma unroll
-  for (int l = 0; l < NZ; ++l)
-    g.Z[l] = __builtin_amdgcn_raw_buffer_load_b128(E.zrs, zv[l], zoff + (uint32_t)gu * unit_z, 0);
+  for (int l = 0; l < NZ; ++l) g.Z[l] = __builtin_amdgcn_raw_buffer_load_b128(E.zrs, c.zv[l], zs, 0);
   return g;
 }
 
@@ -519,14 +511,9 @@ __device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1
   BlockInfo cur = stream_info(E, blk0);
   BlockInfo nxt = stream_info(E, blk1);
   if (cur.G4 == 0) return;
-  // Load contexts of cur and nxt, replaced only at block ends (uniform);
-  // past the last block nxt repeats cur's context with G4 = 0.
-  LoadCtx cc = stream_ctx<MW>(E, cur);
-  LoadCtx nc = nxt.G4 > 0 ? stream_ctx<MW>(E, nxt) : cc;
-  nc.G4 = nxt.G4;
-  uint32_t zv[NZ];
-  stream_zlane<SB, NZ>(E, cread(E.P.info).zrow, zv);
-  int la = 0;                   // next unit to load, counted from the start of cur
+  LoadCtx<NZ> lc = stream_ctx<MW, SB, NZ>(E, cur);
+  bool lnext = false;           // the load cursor is in nxt
+  int lgu = 0;                  // next unit to load
   int pgu = 0;                  // next unit of cur to decode
   int bseq = 0;                 // blocks finished by this workgroup
   UnitRegs<MW, NZ> R[D];
@@ -537,29 +524,27 @@ __device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1
   Scales4 sc = stream_scales(E, cur);
   stream_phase_wait(E, cur.li);
 
-  // Load unit la of the stream (cur's units, then nxt's; clamped to the
-  // last unit when the work ends there -- reloaded, never decoded) into set
-  // k.  Only scalar selects: no register holds a block-dependent value.
-#define TP_STREAM_ISSUE(k)                                                          \
-  do {                                                                              \
-    const int a = min(la, cc.G4 + nc.G4 - 1);                                       \
-    const bool in_n = a >= cc.G4;                                                   \
-    R[k] = stream_load<MW, NZ>(E, in_n ? nc.path : cc.path, in_n ? nc.member : cc.member, \
-                               in_n ? nc.zoff : cc.zoff, zv, in_n ? a - cc.G4 : a);       \
-    ++la;                                                                           \
+  // Load the cursor's unit into set k, then advance the cursor; at the end
+  // of cur it moves into nxt, at the end of nxt (or of the work) it stays and
+  // reloads its unit (in range, never decoded).
+#define TP_STREAM_ISSUE(k)                                     \
+  do {                                                         \
+    R[k] = stream_load<MW, NZ>(E, lc, lgu);                    \
+    if (lgu + 1 < lc.G4) {                                     \
+      ++lgu;                                                   \
+    } else if (!lnext && nxt.G4 > 0) {                         \
+      lc = stream_ctx<MW, SB, NZ>(E, nxt);                     \
+      lnext = true;                                            \
+      lgu = 0;                                                 \
+    }                                                          \
   } while (0)
 
 #pragma unroll
   for (int k = 0; k < D - 1; ++k) TP_STREAM_ISSUE(k);
 
-  // (Leaving through a flag rather than a return keeps every loop-carried
-  // value defined on all paths; a return here costs a dozen extra
-  // instructions per unit.)
-  bool done = false;
-  while (!done) {
+  for (;;) {
 #pragma unroll
     for (int k = 0; k < D; ++k) {
-      if (done) break;
       TP_STREAM_ISSUE((k + D - 1) % D);
       // Halo: word 1 of the previous segment comes from the lane 16 below
       // (K block q-1); lanes of K block 0 take the previous unit's last
@@ -603,10 +588,7 @@ __device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1
           __syncthreads();
           if (E.tid == 0) atomicAdd(&E.pdone[cread(E.P.lphase + cur.li)], 1u);
         }
-        if (nxt.G4 == 0) {
-          done = true;
-          continue;
-        }
+        if (nxt.G4 == 0) return;
         // nxt becomes cur; the ticket claimed during this block names the
         // block after it (double-buffered slot: a slot is rewritten two
         // block ends later, after every wave has read it).
@@ -615,12 +597,9 @@ __device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1
         const int blk = __builtin_amdgcn_readfirstlane(s_tk[bseq & 1]);
         ++bseq;
         if (E.tid == 0 && blk < E.total) pend = atomicAdd(&E.C->ticket, 1u);
-        la -= cur.G4;
         cur = nxt;
-        cc = nc;
         nxt = stream_info(E, blk);
-        if (nxt.G4 > 0) nc = stream_ctx<MW>(E, nxt);
-        nc.G4 = nxt.G4;
+        lnext = false;  // the load cursor is in the new cur
         pgu = 0;
         sc = stream_scales(E, cur);
         stream_phase_wait(E, cur.li);
@@ -630,10 +609,7 @@ __device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1
 #undef TP_STREAM_ISSUE
 }
 
-// Register sets of the stream: 4 (3 units of loads in flight) for SB = 4;
-// 2 for SB = 8 (four z loads per unit) and for plans with a linear shorter
-// than 3 units of K.
-constexpr int kStreamDepth = 4;
+constexpr int kStreamDepth = 4;  // unit register sets of the stream (plans whose K >= 3 units)
 
 // Persistent stream of units: the workgroup walks its blocks (tickets claimed
 // two blocks ahead) and every wave streams its tile's units with D - 1 units
@@ -644,7 +620,7 @@ constexpr int kStreamDepth = 4;
 // unconditionally (after the last block, an in-range unit is reloaded and
 // never used), so the number of loads in flight is the same on every path
 // and each wait covers the oldest register set only.
-template <int KB, int NS, int SB, int D>
+template <int KB, int NS, int SB>
 __global__ void __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(4)))
 tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
                       const uint16_t* __restrict__ codebook, int ordered, int spin_limit) {
@@ -658,9 +634,7 @@ tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
   E.zbuf = plan_rw + E.P.zbuf;
   E.C = reinterpret_cast<StackCounters*>(plan_rw);
   E.pdone = reinterpret_cast<uint32_t*>(plan_rw + E.P.pdone);
-  // not a plan this kernel can run (batch too large, no z buffer, a block
-  // shorter than the stream's lookahead): refuse uniformly
-  if (E.batch > SB || cread(E.P.info).n_rot <= 0 || cread(E.P.info).min_g4 < D - 1) {
+  if (E.batch > SB || cread(E.P.info).n_rot <= 0) {  // not a plan for this kernel
     if (threadIdx.x == 0 && blockIdx.x == 0) atomicExch(&E.C->error, 2u);
     return;
   }
@@ -692,7 +666,13 @@ tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
   const int blk1 = __builtin_amdgcn_readfirstlane(s_tk[1]);
   uint32_t pend = 0;  // thread 0: ticket of the block after blk1
   if (E.tid == 0) pend = atomicAdd(&E.C->ticket, 1u);
-  slot_stream<KB, NS, SB, D>(E, blk0, blk1, pend, s_tk);
+  // Register sets: 4 for 4 z columns per lane set (SB = 4), 2 for SB = 8
+  // (four z loads per unit); 2 when a block is shorter than the pipeline.
+  constexpr int DMAX = SB <= 4 ? kStreamDepth : 2;
+  if (cread(E.P.info).min_g4 >= DMAX - 1)
+    slot_stream<KB, NS, SB, DMAX>(E, blk0, blk1, pend, s_tk);
+  else
+    slot_stream<KB, NS, SB, 2>(E, blk0, blk1, pend, s_tk);
 
   // The last workgroup out resets the counters for the next launch.
   if (E.tid == 0) {
@@ -863,18 +843,6 @@ inline int stack_z_rows(int64_t batch) { return batch <= 16 ? 16 : 32; }
 
 inline int slot_batch(int64_t batch) { return batch <= 4 ? 4 : 8; }
 
-// Shortest K (in units) of each plan initialised in this process, so that a
-// run can pick the stream depth without reading the plan back (a plan the
-// process did not initialise gets the shallow stream).
-std::mutex g_plan_mutex;
-std::unordered_map<const void*, int> g_plan_min_units;
-
-inline int plan_min_units(const void* plan) {
-  std::lock_guard<std::mutex> lock(g_plan_mutex);
-  const auto it = g_plan_min_units.find(plan);
-  return it == g_plan_min_units.end() ? 0 : it->second;
-}
-
 template <int KB, int NS>
 int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t* cb, int ordered,
                 int spin_limit, hipStream_t s) {
@@ -884,15 +852,12 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
   const int grid = (int)(total_blocks < (int64_t)cus * per_cu ? total_blocks : (int64_t)cus * per_cu);
   if (batch <= kSlotMaxBatch) {
     const int sb = slot_batch(batch);
-    if (sb == 4 && plan_min_units(plan) >= kStreamDepth - 1)
-      hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 4, kStreamDepth>), dim3(grid), dim3(kGroupThreads), 0, s,
-                         ro, plan, cb, ordered, spin_limit);
-    else if (sb == 4)
-      hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 4, 2>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan,
-                         cb, ordered, spin_limit);
+    if (sb == 4)
+      hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 4>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
+                         ordered, spin_limit);
     else
-      hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 8, 2>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan,
-                         cb, ordered, spin_limit);
+      hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 8>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
+                         ordered, spin_limit);
   } else {
     const int zr = stack_z_rows(batch);
     const size_t zbytes = (size_t)zr * kZCols * 2;
@@ -909,16 +874,15 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
 // Host-side sizes of a stack (validated); zbuf_bytes and n_rot are 0 for batch > 8.
 struct StackSizes {
   int n_phases;
-  int64_t total_blocks, n_rot, zbuf_bytes, min_g4, zrow;
+  int64_t total_blocks, n_rot, zbuf_bytes, min_g4;
 };
 
-// z rows of one linear: batch rows of the plan's common row length (halves).
-inline int64_t zbuf_linear_bytes(int64_t batch, int64_t zrow) { return (batch * zrow * 2 + 255) & ~(int64_t)255; }
+inline int64_t zbuf_linear_bytes(int64_t batch, int64_t G4) { return (batch * G4 * kChunkCols * 2 + 255) & ~(int64_t)255; }
 
 inline int stack_sizes(const tp_stack_linear* linears, int n_linears, int bits, int64_t batch, StackSizes* out) {
   if (!linears) return TP_ERR_NULL_POINTER;
   if (n_linears < 1 || n_linears > kStackMaxLinears || batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
-  StackSizes z = {1, 0, 0, 0, INT32_MAX, 0};
+  StackSizes z = {1, 0, 0, 0, INT32_MAX};
   for (int i = 0; i < n_linears; ++i) {
     const tp_stack_linear& l = linears[i];
     if (l.phase < 0 || l.phase >= kStackMaxPhases) return TP_ERR_BAD_DIMS;
@@ -931,10 +895,11 @@ inline int stack_sizes(const tp_stack_linear* linears, int n_linears, int bits, 
     if (blocks >= (1 << kStackBlockBits)) return TP_ERR_BAD_DIMS;
     z.total_blocks += blocks;
     if (g.G4 < z.min_g4) z.min_g4 = g.G4;
-    if (g.G4 * kChunkCols > z.zrow) z.zrow = g.G4 * kChunkCols;
-    if (batch <= kSlotMaxBatch) z.n_rot += batch * rot_tiles((int)g.G4);
+    if (batch <= kSlotMaxBatch) {
+      z.n_rot += batch * rot_tiles((int)g.G4);
+      z.zbuf_bytes += zbuf_linear_bytes(batch, g.G4);
+    }
   }
-  if (batch <= kSlotMaxBatch) z.zbuf_bytes = zbuf_linear_bytes(batch, z.zrow) * n_linears;
   // z buffer offsets are 32-bit and lanes past the batch read at 2^31: keep it below 2 GiB
   if (z.total_blocks > INT32_MAX / 2 || z.n_rot > INT32_MAX || z.zbuf_bytes >= ((int64_t)1 << 31))
     return TP_ERR_BAD_DIMS;
@@ -1025,7 +990,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     if (z.zbuf_bytes) {
       for (int64_t j = 0; j < batch * rot_tiles((int)g.G4); ++j) rot_lin[rot + j] = i;
       rot += batch * rot_tiles((int)g.G4);
-      zoff += zbuf_linear_bytes(batch, z.zrow);
+      zoff += zbuf_linear_bytes(batch, g.G4);
     }
   }
   if (st == TP_OK) {
@@ -1045,13 +1010,8 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     h->batch = (int32_t)batch;
     h->n_rot = (int32_t)rot;
     h->min_g4 = (int32_t)z.min_g4;
-    h->zrow = (int32_t)z.zrow;
     h->zbuf_bytes = z.zbuf_bytes;
     if (hipMemcpy(plan, host, lay.zbuf, hipMemcpyHostToDevice) != hipSuccess) st = TP_ERR_HIP;
-  }
-  {
-    std::lock_guard<std::mutex> lock(g_plan_mutex);
-    if (st == TP_OK) g_plan_min_units[plan] = (int)z.min_g4; else g_plan_min_units.erase(plan);
   }
   free(host);
   return st;
