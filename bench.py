@@ -282,7 +282,7 @@ def main() -> int:
                    "bytes_per_step": nbytes},
         "gbps": round(gbps, 1), "pct_hbm_peak": round(100 * gbps / HBM_PEAK_GBPS, 2),
         "wall_ms_per_step": round(ms_wall, 5),
-        "roofline": {"kernel": "tcq_stack_slot_kernel<3,64,4,4> (all 252 linears, one launch per step)",
+        "roofline": {"kernel": "tcq_stack_slot_kernel<3,64,4> (all 252 linears, one launch per step)",
                      "bound": "hbm", "achieved": round(gemv_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(gemv_gbps / HBM_PEAK_GBPS, 4), "traffic": measured_traffic(),
                      "us_per_launch": round(us_gemv, 2), "bytes_per_launch": gemv_bytes},
