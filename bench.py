@@ -25,8 +25,11 @@ PackedTCQLinear.forward path).
 (tcq_stack_slot_kernel): its algorithmic bytes (the step's bytes minus the
 rot_scale vectors, which only the rotation launch reads) over its own
 duration, timed with HIP events around back-to-back launches on the stream
-they run on.  ``cpu_baseline`` times the reference's CPU tiled path (the
-oracle's op-for-op restatement) on a bounded sample on this host.
+they run on.  ``read_reference`` is a plain streaming read of the step's
+byte count (``tp_read_probe``): the read bandwidth the box reaches with no
+compute, i.e. the practical ceiling the kernel is compared against.
+``cpu_baseline`` times the reference's CPU tiled path (the oracle's
+op-for-op restatement) on a bounded sample on this host.
 """
 
 from __future__ import annotations
@@ -168,6 +171,34 @@ def copy_reference(mib: int, reps: int = 10):
             "gbps": round(moved / (us * 1e-6) / 1e9, 1)}
 
 
+def read_reference(nbytes: int, reps: int = 20):
+    """A plain streaming read (tp_read_probe: grid-stride 16-byte loads, no
+    compute) of as many bytes as one step moves: the read bandwidth this box
+    reaches at all, i.e. the practical ceiling of an HBM-bound read stream."""
+    from turbopress_amd import _lib
+    lib = _lib.lib()
+    nbytes = (nbytes + 15) & ~15
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device="cuda")
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run():
+        _lib.check(lib.tp_read_probe(buf.data_ptr(), nbytes, sink.data_ptr(), stream), "read_probe")
+
+    for _ in range(reps):
+        run()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        run()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) / reps * 1e3
+    del buf, sink
+    return {"bytes_read": nbytes, "us": round(us, 2), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1)}
+
+
 def cpu_baseline(budget_s: float):
     """The reference's CPU tiled path (oracle restatement), one Qwen3-4B layer
     at k=3, B=1, repeated until ~budget_s of CPU work, scaled to 36 layers."""
@@ -263,6 +294,8 @@ def main() -> int:
     copy_ref = copy_reference(args.copy_mib) if args.copy_mib > 0 else None
     if copy_ref:
         log(f"device copy {args.copy_mib} MiB: {copy_ref['gbps']} GB/s (read + write)")
+    read_ref = read_reference(nbytes)
+    log(f"streaming read of {nbytes / 1e9:.4f} GB: {read_ref['us']} us, {read_ref['gbps']} GB/s")
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline")
@@ -288,6 +321,7 @@ def main() -> int:
                      "us_per_launch": round(us_gemv, 2), "bytes_per_launch": gemv_bytes},
         "executors": extra,
         "copy_reference": copy_ref,
+        "read_reference": read_ref,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

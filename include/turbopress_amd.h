@@ -48,6 +48,15 @@ const char* tp_status_string(int status);
  * counterpart (the reference times with host clocks, scripts/bench_packed.py). */
 int tp_device_delay(int64_t microseconds, void* stream);
 
+/* Read `bytes` (a multiple of 16, 16-byte aligned) of device memory once
+ * with a plain streaming-read kernel (grid-stride 16-byte loads, 4
+ * workgroups per CU); `sink` (one device word) is written only in the
+ * practically impossible case that the XOR of all words hits a constant.
+ * Benchmark utility: the achievable read bandwidth of the GPU it runs on,
+ * the practical ceiling of an HBM-bound read stream.  No reference
+ * counterpart. */
+int tp_read_probe(const void* buf, int64_t bytes, uint32_t* sink, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Trellis tables (host only, no GPU work)
  * ------------------------------------------------------------------------- */

@@ -70,6 +70,9 @@ def test_host_side_argument_validation(built_lib):
         == _lib.TP_ERR_BAD_DIMS
     assert built_lib.tp_tcq_gemv(fake, 1, fake, 12, None, 24, fake, fake, None, 4, 96, 3, 64,
                                  fake, None) == _lib.TP_ERR_NULL_POINTER
+    assert built_lib.tp_read_probe(None, 64, fake, None) == _lib.TP_ERR_NULL_POINTER
+    assert built_lib.tp_read_probe(fake, 20, fake, None) == _lib.TP_ERR_BAD_DIMS
+    assert built_lib.tp_read_probe(ctypes.c_void_p(24), 64, fake, None) == _lib.TP_ERR_MISALIGNED
 
 
 def test_check_maps_status_to_reference_exceptions():

@@ -154,3 +154,19 @@ def test_packed_bytes_and_attributes(cuda):
     assert cached.path_packed is None and cached._w_cache is not None
     assert hip.packed_bytes() < 2 * 256 * 256 / 6
     assert cached.packed_bytes() >= 2 * 256 * 256
+
+
+@pytest.mark.gpu
+def test_read_probe_runs_and_checks_arguments(cuda):
+    """The streaming-read probe reads a buffer without writing it (its sink
+    stays zero for an all-zero buffer) and rejects sizes that are not whole
+    16-byte words."""
+    from turbopress_amd import _lib
+    lib = _lib.lib()
+    buf = torch.zeros(1 << 20, dtype=torch.int32, device=cuda)
+    sink = torch.zeros(1, dtype=torch.int32, device=cuda)
+    stream = torch.cuda.current_stream(cuda).cuda_stream
+    assert lib.tp_read_probe(buf.data_ptr(), buf.numel() * 4, sink.data_ptr(), stream) == 0
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 0
+    assert lib.tp_read_probe(buf.data_ptr(), 20, sink.data_ptr(), stream) != 0

@@ -95,6 +95,20 @@ inline int check_bits(int bits) {
   return (bits >= 1 && bits <= 7) ? TP_OK : TP_ERR_UNSUPPORTED_BITS;
 }
 
+// CUs of the current device (cached per device; 256 if the query fails).
+inline int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? TP_OK : TP_ERR_HIP;

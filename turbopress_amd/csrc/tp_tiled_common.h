@@ -463,18 +463,6 @@ inline int tiled_geom(int64_t n, int64_t d, int bits, Geom* g) {
   return TP_OK;
 }
 
-inline int device_cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (!cached[dev]) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-    cached[dev] = cus;
-  }
-  return cached[dev];
-}
 
 
 // One unit (16 rows x 4 segments) of one wave: halo exchange, decode of the
