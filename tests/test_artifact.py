@@ -1,0 +1,138 @@
+"""Format-v1 artifacts: v1 -> v2 conversion (bit-exact against the oracle),
+the loader's guards, and (GPU) a synthetic artifact loaded into a packed
+Qwen3 model and decoded greedily with and without graph capture
+(runtime.py:417-541, tests/test_run.py:20-79, scripts/graph_decode_bench.py)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import tcq_oracle as O
+from turbopress_amd.artifact import load_packed_model, v1_payload_to_packed, v1_stream_to_rows
+from turbopress_amd.synthetic import make_v1_payload
+
+
+def _v1_pack(vals: np.ndarray, width: int) -> np.ndarray:
+    """Independent format-v1 packer: value p's bit j at flat stream bit
+    p*width + j, stream bits MSB-first within each byte (pipeline.py:106-111)."""
+    flat = vals.reshape(-1).astype(np.uint8)
+    bits = ((flat[:, None] >> np.arange(width, dtype=np.uint8)) & 1).reshape(-1)
+    return np.packbits(bits)
+
+
+@pytest.mark.parametrize("width", [1, 2, 3])
+@pytest.mark.parametrize("n,d", [(7, 100), (5, 64), (3, 9)])
+def test_v1_stream_to_rows_regroups_per_row(width, n, d):
+    rng = np.random.default_rng(width * 100 + d)
+    vals = rng.integers(0, 1 << width, size=(n, d), dtype=np.uint8)
+    rows = v1_stream_to_rows(_v1_pack(vals, width), n, d, width)
+    assert rows.shape == (n, (d * width + 7) // 8)
+    assert np.array_equal(rows, O.pack_le(vals, width))
+    assert np.array_equal(O.unpack_le(rows, d, width), vals)
+    # the oracle's reading of the v1 stream agrees with the packer above
+    assert np.array_equal(O.unpack_bits_v1(_v1_pack(vals, width), n * d, width).reshape(n, d), vals)
+
+
+def test_v1_stream_too_short_raises():
+    with pytest.raises(ValueError):
+        v1_stream_to_rows(np.zeros(3, np.uint8), 2, 16, 1)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_v1_payload_to_packed_keeps_every_code(bits):
+    """No re-quantization: the v2 payload carries exactly the artifact's codes,
+    scales, codebook, signs and 1/equil (runtime.py:437-452)."""
+    n, d = 48, 192
+    v1 = make_v1_payload(n, d, bits, 64, seed=bits)
+    bias = torch.randn(n)
+    v2 = v1_payload_to_packed(v1, bias, "cpu")
+    assert v2["format"] == 2 and (v2["n"], v2["d"], v2["bits"], v2["n_states"]) == (n, d, bits, 64)
+    assert v2["block"] == 64
+    path = O.unpack_bits_v1(v1["path_bits"].numpy(), n * d, 1).reshape(n, d)
+    assert np.array_equal(O.unpack_le(v2["path_packed"].numpy(), d, 1), path)
+    member = O.unpack_bits_v1(v1["member_bits"].numpy(), n * d, bits - 1).reshape(n, d)
+    assert np.array_equal(O.unpack_le(v2["member_packed"].numpy(), d, bits - 1), member)
+    signs = O.unpack_bits_v1(v1["signs"].numpy(), d, 1)
+    assert np.array_equal(O.unpack_le(v2["signs_packed"].numpy(), d, 1)[0], signs)
+    want_inv = (1.0 / v1["equil"].float().clamp_min(1e-12)).to(torch.float16)
+    assert torch.equal(v2["inv_equil"], want_inv)
+    assert torch.equal(v2["scales"], v1["scales"]) and torch.equal(v2["codebook"], v1["codebook"])
+    assert torch.equal(v2["bias"], bias.to(torch.float16))
+    # and the decoded weights are those of the v1 codes
+    lv = O.window_decode_levels(path, member, 64)
+    np.testing.assert_array_equal(O.levels_of({k: (v.numpy() if isinstance(v, torch.Tensor) else v)
+                                               for k, v in v2.items()}), lv)
+
+
+def test_load_packed_model_guards(tmp_path):
+    with pytest.raises(ValueError):
+        load_packed_model("anywhere", device="cpu", mode="nope")
+    with pytest.raises(FileNotFoundError):
+        load_packed_model(tmp_path, device="cpu", mode="hip")
+    torch.save({"meta": {"format_version": 2, "n_states": 64, "generators": [0o133, 0o171]},
+                "quantized": {}, "extra_state": {}}, tmp_path / "turbopress_weights.pt")
+    with pytest.raises(RuntimeError, match="format_version"):
+        load_packed_model(tmp_path, device="cpu", mode="hip")
+    torch.save({"meta": {"format_version": 1, "n_states": 64, "generators": [0o23, 0o35]},
+                "quantized": {}, "extra_state": {}}, tmp_path / "turbopress_weights.pt")
+    with pytest.raises(RuntimeError, match="generator"):
+        load_packed_model(tmp_path, device="cpu", mode="hip")
+    torch.save({"meta": {"format_version": 1, "n_states": 64, "generators": [0o133, 0o171]},
+                "quantized": {}, "extra_state": {}}, tmp_path / "turbopress_weights.pt")
+    with pytest.raises(RuntimeError, match="GPU"):
+        load_packed_model(tmp_path, device="cpu", mode="hip")
+
+
+# ---------------------------------------------------------------------------
+# GPU: a synthetic artifact end to end
+# ---------------------------------------------------------------------------
+@pytest.fixture(scope="module")
+def tiny_artifact(tmp_path_factory):
+    from turbopress_amd.synthetic import tiny_qwen3_config, write_synthetic_artifact
+    root = tmp_path_factory.mktemp("artifact")
+    write_synthetic_artifact(root, tiny_qwen3_config(), bits=3, n_states=64, seed=0)
+    return root
+
+
+@pytest.mark.gpu
+def test_load_packed_model_replaces_every_decoder_linear(cuda, tiny_artifact):
+    from turbopress_amd.artifact import decoder_layers
+    from turbopress_amd.runtime import PackedTCQLinear
+    model, meta = load_packed_model(tiny_artifact, device="cuda", mode="hip")
+    assert meta["format_version"] == 1 and meta["n_states"] == 64
+    packed = [m for blk in decoder_layers(model) for m in blk.modules() if isinstance(m, PackedTCQLinear)]
+    assert len(packed) == 7 * len(decoder_layers(model))
+    assert all(m.mode == "hip" and m.tiled_packed is not None for m in packed)
+    assert model.lm_head.weight.data_ptr() == model.model.embed_tokens.weight.data_ptr()  # still tied
+
+
+@pytest.mark.gpu
+def test_packed_model_logits_hip_vs_cached(cuda, tiny_artifact):
+    """The bandwidth path (fused rotation + decode-GEMV) and load-time
+    decompression (decode + fold + GEMM) give the same model."""
+    ids = torch.randint(0, 1024, (1, 12), generator=torch.Generator().manual_seed(0)).to(cuda)
+    outs = {}
+    for mode in ("hip", "cached"):
+        model, _ = load_packed_model(tiny_artifact, device="cuda", mode=mode)
+        with torch.inference_mode():
+            outs[mode] = model(input_ids=ids).logits.float()
+        del model
+    a, b = outs["hip"], outs["cached"]
+    assert torch.isfinite(a).all()
+    rel = ((a - b).abs().max() / b.abs().max()).item()
+    assert rel < 2e-2, rel
+    assert torch.equal(a[0, -1].argmax(), b[0, -1].argmax()) or rel < 5e-3
+
+
+@pytest.mark.gpu
+def test_graph_decode_matches_eager(cuda, tiny_artifact):
+    """One captured decode step replayed per token yields the eager loop's
+    greedy tokens (graph_decode_bench.py:135-141)."""
+    from turbopress_amd.graph_decode import decode_eager, decode_graph
+    model, _ = load_packed_model(tiny_artifact, device="cuda", mode="hip")
+    ids = torch.randint(0, 1024, (1, 8), generator=torch.Generator().manual_seed(1)).to(cuda)
+    n_new, max_len = 16, 8 + 16 + 8
+    toks_e, _ = decode_eager(model, ids, n_new, max_len)
+    toks_g, _ = decode_graph(model, ids, n_new, max_len)
+    assert len(toks_e) == len(toks_g) == n_new
+    assert toks_e == toks_g

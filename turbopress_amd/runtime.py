@@ -31,11 +31,19 @@ from torch import Tensor, nn
 
 from turbopress_amd import hip_kernel as hk
 
-__all__ = ["PackedTCQLinear", "MODES", "Trellis"]
+__all__ = ["PackedTCQLinear", "MODES", "Trellis", "trellis_generators"]
 
 MODES = ("hip", "triton", "cached", "tiled")
 
 _GENERATORS = {4: (0o5, 0o7), 8: (0o15, 0o17), 16: (0o23, 0o35), 64: (0o133, 0o171)}
+
+
+def trellis_generators(n_states: int) -> tuple[int, int]:
+    """(g0, g1) of the S-state bitshift trellis (trellis.py:47-52); artifacts
+    record them so a loader can refuse an incompatible trellis."""
+    if n_states not in _GENERATORS:
+        raise ValueError(f"n_states must be one of {sorted(_GENERATORS)}, got {n_states}")
+    return _GENERATORS[n_states]
 
 
 class Trellis:
@@ -200,6 +208,18 @@ class PackedTCQLinear(nn.Module):
             if self.bias is not None:
                 y = y + self.bias
         return y.to(x.dtype)
+
+    def _apply(self, fn, recurse=True):
+        """Device moves apply; dtype casts of the whole model (``.half()``,
+        ``.to(dtype=...)``) leave the packed buffers in the fp16/uint8 storage
+        the kernels read."""
+        dtypes = {name: b.dtype for name, b in self._buffers.items() if b is not None}
+        super()._apply(fn, recurse)
+        for name, dt in dtypes.items():
+            b = self._buffers.get(name)
+            if b is not None and b.dtype != dt:
+                self._buffers[name] = b.to(dt)
+        return self
 
     # -- accounting ---------------------------------------------------------
     def packed_bytes(self) -> int:

@@ -124,3 +124,79 @@ def payload_numpy(payload: dict) -> dict:
     """Copy of a payload with every tensor as a CPU numpy array."""
     return {k: (v.detach().cpu().numpy() if isinstance(v, torch.Tensor) else v)
             for k, v in payload.items()}
+
+
+# ---------------------------------------------------------------------------
+# format-v1 matrices and artifacts (the pipeline's on-disk format)
+# ---------------------------------------------------------------------------
+def make_v1_payload(n: int, d: int, bits: int, n_states: int = 64, seed: int = 0) -> dict:
+    """A seeded format-v1 matrix (pipeline.py:445-455): flat MSB-first code
+    streams over the whole matrix (uniform bytes are legal codes), fp16 scales,
+    packed Rademacher signs, fp16 equilibration and the default codebook."""
+    gen = torch.Generator().manual_seed(seed)
+
+    def flat(nbits: int) -> torch.Tensor:
+        return torch.randint(0, 256, ((nbits + 7) // 8,), generator=gen, dtype=torch.uint8)
+
+    path = flat(n * d)
+    member = flat(n * d * (bits - 1)) if bits > 1 else None
+    scales = (torch.randn(n, generator=gen).abs() * 0.02 + 1e-3).to(torch.float16)
+    equil = torch.exp(torch.randn(d, generator=gen) * 0.25).to(torch.float16)
+    signs = flat(d)
+    if (bits, n_states) in available_codebooks():
+        cb = default_codebook(bits, n_states)
+    else:
+        cb = _synthetic_codebook(bits, seed)
+    return {"n": n, "d": d, "block": d & -d, "bits": bits, "n_states": n_states,
+            "path_bits": path, "member_bits": member, "scales": scales, "signs": signs,
+            "equil": equil, "codebook": cb}
+
+
+def tiny_qwen3_config(layers: int = 2, hidden: int = 256, intermediate: int = 768, heads: int = 4,
+                      kv_heads: int = 2, head_dim: int = 64, vocab: int = 1024):
+    """A small Qwen3 decoder configuration (random weights only: no checkpoint
+    is ever downloaded)."""
+    from transformers import Qwen3Config
+    return Qwen3Config(vocab_size=vocab, hidden_size=hidden, intermediate_size=intermediate,
+                       num_hidden_layers=layers, num_attention_heads=heads, num_key_value_heads=kv_heads,
+                       head_dim=head_dim, max_position_embeddings=512, tie_word_embeddings=True,
+                       torch_dtype="float16")
+
+
+def write_synthetic_artifact(root, config, bits: int = 3, n_states: int = 64, seed: int = 0) -> dict:
+    """Write a TurboPress format-v1 artifact directory for a randomly
+    initialised model of `config` (pipeline.py:917-931 layout:
+    ``turbopress_weights.pt`` = {meta, quantized, extra_state} and
+    ``hf_config/``); every decoder linear is a seeded v1 matrix.  Returns the
+    metadata."""
+    from pathlib import Path
+
+    from torch import nn
+    from transformers import AutoModelForCausalLM
+
+    from turbopress_amd.artifact import decoder_layers
+    from turbopress_amd.runtime import trellis_generators
+
+    root = Path(root)
+    root.mkdir(parents=True, exist_ok=True)
+    torch.manual_seed(seed)
+    model = AutoModelForCausalLM.from_config(config).to(torch.float16)
+    quantized = {}
+    prefix = None
+    for name, _ in model.named_modules():
+        if name.endswith(".layers") or name.endswith(".h"):
+            prefix = name
+            break
+    layers = decoder_layers(model)
+    for i, block in enumerate(layers):
+        for name, mod in block.named_modules():
+            if isinstance(mod, nn.Linear):
+                key = f"{prefix}.{i}.{name}.weight"
+                quantized[key] = make_v1_payload(mod.out_features, mod.in_features, bits, n_states,
+                                                 seed=seed * 1000 + len(quantized))
+    extra = {k: v for k, v in model.state_dict().items() if k not in quantized and k != "lm_head.weight"}
+    meta = {"format_version": 1, "model_id": "synthetic", "bits": bits, "n_states": n_states,
+            "generators": list(trellis_generators(n_states)), "seed": seed}
+    torch.save({"meta": meta, "quantized": quantized, "extra_state": extra}, root / "turbopress_weights.pt")
+    config.save_pretrained(root / "hf_config")
+    return meta
