@@ -34,6 +34,8 @@
 #include "tp_tiled_common.h"
 
 #include <algorithm>
+#include <mutex>
+#include <unordered_map>
 #include <type_traits>
 #include <vector>
 
@@ -46,9 +48,10 @@ constexpr int kSlotMaxBatch = 8;             // batches up to this use the slot 
 
 // Plan layout (device memory):
 //   [0, 64)             StackCounters  -- written by the kernels (atomics)
-//   [64, ...)           StackInfo, LinearDesc[n_lin], prefix[n_lin+1],
+//   [64, ...)           StackInfo, RotItem[n_rot] (at the fixed offset
+//                       kRotItems), LinearDesc[n_lin], prefix[n_lin+1],
 //                       lphase[n_lin], pblocks[n_phases], sched_ordered[total],
-//                       sched_unordered[total], rot_prefix[n_lin+1]  -- read-only
+//                       sched_unordered[total]  -- read-only
 //   [pdone, ...)        pdone[n_phases] -- written by the kernel (atomics)
 //   [zbuf, ...)         rotated activations, batch <= 8 plans only
 // The read-only part is passed as a separate const __restrict__ argument so
@@ -70,11 +73,29 @@ struct StackInfo {
   int64_t zbuf_bytes;
 };
 
+// One rotation tile (4096 columns of one batch row of one linear's input),
+// self-contained so that the rotation kernel starts from a single scalar
+// load: input row, rot_scale and z row bases, tile index and the linear's
+// sizes.
+struct RotItem {
+  const uint16_t* x;    // input row (x + b * ldx)
+  const uint16_t* rs;   // rot_scale [d]
+  uint16_t* z;          // z row in the plan's z buffer
+  int32_t k;            // tile index along d
+  int32_t d;
+  int32_t hb;           // Hadamard block
+  int32_t zld;          // z columns written (G4 * 256; zero past d)
+  float hdiv;           // fp32(sqrt(hb))
+  int32_t reserved[5];
+};
+static_assert(sizeof(RotItem) == 64, "one 16-dword scalar load per rotation tile");
+
 struct StackLayout {
-  size_t lin, prefix, lphase, pblocks, sched_o, sched_u, rot_prefix, rot_lin, pdone, zbuf, total;
+  size_t rot_items, lin, prefix, lphase, pblocks, sched_o, sched_u, pdone, zbuf, total;
 };
 
 constexpr size_t kStackRO = sizeof(StackCounters);
+constexpr size_t kRotItems = (kStackRO + sizeof(StackInfo) + 63) & ~(size_t)63;  // fixed offset
 
 // Reads of the plan's read-only part through the constant address space:
 // the plan does not change during a launch, so wave-uniform reads become
@@ -89,7 +110,9 @@ __device__ __forceinline__ const TP_CONST T& cread(const T* p) {
 __host__ __device__ inline StackLayout stack_layout(int n_lin, int n_phases, int total_blocks, int n_rot,
                                                     int64_t zbuf_bytes) {
   StackLayout p;
-  size_t o = kStackRO + sizeof(StackInfo);
+  size_t o = kRotItems;
+  p.rot_items = o;
+  o += sizeof(RotItem) * (size_t)n_rot;
   p.lin = o;
   o += sizeof(LinearDesc) * (size_t)n_lin;
   p.prefix = o;
@@ -102,10 +125,6 @@ __host__ __device__ inline StackLayout stack_layout(int n_lin, int n_phases, int
   o += sizeof(int32_t) * (size_t)total_blocks;
   p.sched_u = o;
   o += sizeof(int32_t) * (size_t)total_blocks;
-  p.rot_prefix = o;
-  o += sizeof(int32_t) * (size_t)(n_lin + 1);
-  p.rot_lin = o;
-  o += sizeof(int32_t) * (size_t)n_rot;
   o = (o + 63) & ~(size_t)63;
   p.pdone = o;
   o += sizeof(uint32_t) * (size_t)n_phases;
@@ -124,8 +143,6 @@ struct StackRO {  // views into the read-only part
   const int32_t* pblocks;  // [n_phases] blocks per phase
   const int32_t* sched_o;  // [total] (linear << 20) | block, phase order
   const int32_t* sched_u;  // [total] same blocks, longest K first
-  const int32_t* rot_prefix;  // [n_lin + 1] first rotation item of each linear
-  const int32_t* rot_lin;     // [n_rot] linear of each rotation item
   size_t pdone;            // byte offset of pdone from the plan start
   size_t zbuf;             // byte offset of the z buffer from the plan start
 };
@@ -143,8 +160,6 @@ __device__ inline StackRO stack_ro(const char* __restrict__ ro) {
   v.pblocks = reinterpret_cast<const int32_t*>(ro + (l.pblocks - kStackRO));
   v.sched_o = reinterpret_cast<const int32_t*>(ro + (l.sched_o - kStackRO));
   v.sched_u = reinterpret_cast<const int32_t*>(ro + (l.sched_u - kStackRO));
-  v.rot_prefix = reinterpret_cast<const int32_t*>(ro + (l.rot_prefix - kStackRO));
-  v.rot_lin = reinterpret_cast<const int32_t*>(ro + (l.rot_lin - kStackRO));
   v.pdone = l.pdone;
   v.zbuf = l.zbuf;
   return v;
@@ -213,24 +228,26 @@ __device__ __forceinline__ void load16(__amdgpu_buffer_rsrc_t r, uint32_t off, f
   }
 }
 
+// One workgroup per tile when the host knows the tile count (ONE_TILE: the
+// descriptor is the first load, the x / rot_scale loads the second);
+// otherwise a grid-stride loop bounded by the plan's count.
+template <bool ONE_TILE>
 __global__ void __launch_bounds__(kRotThreads)
 tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
   __shared__ float ex[kRotTile];
-  const StackRO P = stack_ro(plan_ro);
-  const int n_rot = cread(P.info).n_rot;
+  const int first = blockIdx.x;
+  const int end = ONE_TILE ? first + 1 : cread(reinterpret_cast<const StackInfo*>(plan_ro)).n_rot;
+  const int step = ONE_TILE ? 1 : (int)gridDim.x;
+  const RotItem* items = reinterpret_cast<const RotItem*>(plan_ro + (kRotItems - kStackRO));
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  for (int item = blockIdx.x; item < n_rot; item += gridDim.x) {
-    // plan lookups are scalar loads: one dependent load per level
-    const int li = cread(P.rot_lin + item);
-    const TP_CONST LinearDesc& L = cread(P.lin + li);
-    const int ntiles = rot_tiles(L.G4);
-    const int local = item - cread(P.rot_prefix + li);
-    const int b = local / ntiles, k = local - b * ntiles;
+  for (int item = first; item < end; item += step) {
+    const TP_CONST RotItem& L = cread(items + item);
+    const int k = L.k;
     const int c0 = k * kRotTile + tid * kRotEPT;      // first column of this thread
     const int hb = L.hb;
-    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(L.x + (size_t)b * L.ldx, (uint32_t)L.d * 2u);
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(L.x, (uint32_t)L.d * 2u);
     const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(L.rs, (uint32_t)L.d * 2u);
     float v[kRotEPT];
     if (hb <= kRotTile) {
@@ -306,8 +323,8 @@ tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
         }
       }
     }
-    const int zld = L.G4 * kChunkCols;               // columns written (zero past d)
-    uint16_t* zr = L.z + (size_t)b * zld;
+    const int zld = L.zld;                           // columns written (zero past d)
+    uint16_t* zr = L.z;
 #pragma unroll
     for (int g = 0; g < kRotEPT / 4; ++g) {
       if (c0 + 4 * g >= zld) break;
@@ -871,6 +888,17 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
   return launch_status();
 }
 
+// Rotation tile count of each plan initialised in this process (a plan the
+// process did not initialise gets the kernel that reads the count itself).
+std::mutex g_plan_mutex;
+std::unordered_map<const void*, int> g_plan_rot;
+
+inline int plan_rotation_tiles(const void* plan) {
+  std::lock_guard<std::mutex> lock(g_plan_mutex);
+  const auto it = g_plan_rot.find(plan);
+  return it == g_plan_rot.end() ? 0 : it->second;
+}
+
 // Host-side sizes of a stack (validated); zbuf_bytes and n_rot are 0 for batch > 8.
 struct StackSizes {
   int n_phases;
@@ -939,8 +967,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
   int32_t* pblocks = reinterpret_cast<int32_t*>(host + lay.pblocks);
   int32_t* sched_o = reinterpret_cast<int32_t*>(host + lay.sched_o);
   int32_t* sched_u = reinterpret_cast<int32_t*>(host + lay.sched_u);
-  int32_t* rot_prefix = reinterpret_cast<int32_t*>(host + lay.rot_prefix);
-  int32_t* rot_lin = reinterpret_cast<int32_t*>(host + lay.rot_lin);
+  RotItem* items = reinterpret_cast<RotItem*>(host + lay.rot_items);
   char* zbuf = reinterpret_cast<char*>(plan) + lay.zbuf;
   int64_t total = 0, rot = 0, zoff = 0;
   for (int i = 0; i < n_linears; ++i) {
@@ -982,20 +1009,31 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     L.blocks = (int32_t)((g.T + kWavesPerGroup - 1) / kWavesPerGroup);
     L.hb = (int32_t)hb;
     prefix[i] = (int32_t)total;
-    rot_prefix[i] = (int32_t)rot;
     lphase[i] = l.phase;
     pblocks[l.phase] += L.blocks;
     for (int b = 0; b < L.blocks; ++b) sched_o[total + b] = (i << kStackBlockBits) | b;
     total += L.blocks;
     if (z.zbuf_bytes) {
-      for (int64_t j = 0; j < batch * rot_tiles((int)g.G4); ++j) rot_lin[rot + j] = i;
-      rot += batch * rot_tiles((int)g.G4);
+      const int ntiles = rot_tiles((int)g.G4);
+      const int zld = (int)g.G4 * kChunkCols;
+      for (int64_t b = 0; b < batch; ++b) {
+        for (int k = 0; k < ntiles; ++k) {
+          RotItem& R = items[rot++];
+          R.x = l.x + b * l.ldx;
+          R.rs = l.rot_scale;
+          R.z = L.z + b * zld;
+          R.k = k;
+          R.d = (int32_t)l.d;
+          R.hb = (int32_t)hb;
+          R.zld = zld;
+          R.hdiv = L.hdiv;
+        }
+      }
       zoff += zbuf_linear_bytes(batch, g.G4);
     }
   }
   if (st == TP_OK) {
     prefix[n_linears] = (int32_t)total;
-    rot_prefix[n_linears] = (int32_t)rot;
     // Unordered schedule: blocks of the longest K first (stable), so the
     // launch ends on short blocks.
     std::vector<int> order(n_linears);
@@ -1013,6 +1051,10 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     h->zbuf_bytes = z.zbuf_bytes;
     if (hipMemcpy(plan, host, lay.zbuf, hipMemcpyHostToDevice) != hipSuccess) st = TP_ERR_HIP;
   }
+  {
+    std::lock_guard<std::mutex> lock(g_plan_mutex);
+    if (st == TP_OK && z.n_rot > 0) g_plan_rot[plan] = (int)z.n_rot; else g_plan_rot.erase(plan);
+  }
   free(host);
   return st;
 }
@@ -1022,8 +1064,12 @@ extern "C" int tp_stack_rotate(void* plan, int64_t batch, void* stream) {
   if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
   if (batch > kSlotMaxBatch) return TP_OK;  // the LDS kernel rotates on the fly
   const char* ro = reinterpret_cast<const char*>(plan) + kStackRO;
-  hipLaunchKernelGGL(tcq_stack_rotate_kernel, dim3(2 * device_cu_count()), dim3(kRotThreads), 0,
-                     (hipStream_t)stream, ro);
+  const int n_rot = plan_rotation_tiles(plan);
+  if (n_rot > 0)
+    hipLaunchKernelGGL(tcq_stack_rotate_kernel<true>, dim3(n_rot), dim3(kRotThreads), 0, (hipStream_t)stream, ro);
+  else
+    hipLaunchKernelGGL(tcq_stack_rotate_kernel<false>, dim3(2 * device_cu_count()), dim3(kRotThreads), 0,
+                       (hipStream_t)stream, ro);
   return launch_status();
 }
 
