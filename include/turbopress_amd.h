@@ -286,6 +286,30 @@ int tp_decode_tiled(const uint8_t* path_tiled, const uint8_t* member_tiled,
                     int64_t n, int64_t d, int bits, int n_states,
                     uint16_t* w_out, int64_t out_stride, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * TCQ encoder (compress time)
+ * ------------------------------------------------------------------------- */
+
+/* Workspace of tp_tcq_viterbi: one 64-bit branch-decision word per column
+ * and row (n * d * 8 bytes).  Host only. */
+int64_t tp_viterbi_workspace_bytes(int64_t n, int64_t d);
+
+/* Minimum-distortion trellis path of every row of z (fp32 [n, ldz], d
+ * columns used) against the doubled codebook (fp32 [2^(bits+1)], each subset
+ * codebook[j::4] ascending): replaces `_viterbi` (turbopress/trellis.py:
+ * 111-179; pipeline.py:209-276's copy).  Same fp32 arithmetic and
+ * tie-breaking: nearest member = number of subset midpoints strictly below z
+ * (torch.bucketize), branch 1 only if strictly cheaper, end state = first
+ * state of minimum metric.  Each row starts in start_state[row] (NULL:
+ * state 0).  Outputs uint8 [n, d] level codes (member * 4 + subset), path
+ * bits and member codes, and int32 end_state[n] (may be NULL).  bits in
+ * 1..4, n_states in {4, 8, 16, 64}; workspace of
+ * tp_viterbi_workspace_bytes(n, d), 8-byte aligned, contents irrelevant. */
+int tp_tcq_viterbi(const float* z, int64_t ldz, int64_t n, int64_t d, const float* codebook, int bits,
+                   int n_states, const int32_t* start_state, uint8_t* level_codes, uint8_t* path_bits,
+                   uint8_t* member_codes, int32_t* end_state, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -8,7 +8,7 @@ on ``bucketize``, on ``index_add_`` summation order and on the Viterbi
 tie-break, so this restatement uses the same torch calls in the same order.
 
   * ``lloyd_max_gaussian``      codebooks.py:45-81
-  * ``viterbi``                 trellis.py:111-179
+  * ``viterbi`` / ``viterbi_full``  trellis.py:111-179
   * ``tcq_optimized_codebook``  trellis.py:206-253  (65536 samples, 8 iters)
   * ``pipeline_tcq_codebook``   pipeline.py:282-301  (8x8192 samples, 6 iters,
                                 built from pipeline.py's own Lloyd-Max copy)
@@ -96,6 +96,14 @@ class _Tables:
 def viterbi(z: torch.Tensor, codebook: torch.Tensor, n_states: int):
     """trellis.py:111-179: minimum-distortion trellis path per row from state 0.
     Returns (level_codes, path_bits, member_codes) as uint8 [n, d]."""
+    level, pathb, memb, _ = viterbi_full(z, codebook, n_states)
+    return level, pathb, memb
+
+
+def viterbi_full(z: torch.Tensor, codebook: torch.Tensor, n_states: int,
+                 start_state: torch.Tensor | None = None):
+    """trellis.py:128-179 with its optional start state and returned end
+    state: (level_codes, path_bits, member_codes, end_state)."""
     tr = _Tables(n_states)
     n, d = z.shape
     members = torch.empty(n, d, N_SUBSETS, dtype=torch.int64)
@@ -110,7 +118,10 @@ def viterbi(z: torch.Tensor, codebook: torch.Tensor, n_states: int):
         members[:, :, j] = mem
         costs[:, :, j] = (z - sub_cb[mem]).pow(2)
     alpha = torch.full((n, n_states), torch.inf)
-    alpha[:, 0] = 0.0
+    if start_state is None:
+        alpha[:, 0] = 0.0
+    else:
+        alpha[torch.arange(n), start_state.long()] = 0.0
     bp = torch.empty(n, d, n_states, dtype=torch.bool)
     for t in range(d):
         c = costs[:, t, :]
@@ -124,6 +135,7 @@ def viterbi(z: torch.Tensor, codebook: torch.Tensor, n_states: int):
     memb = torch.empty(n, d, dtype=torch.uint8)
     rows = torch.arange(n)
     state = alpha.argmin(dim=1)
+    end_state = state.clone()
     for t in range(d - 1, -1, -1):
         take1 = bp[rows, t, state]
         prev = torch.where(take1, tr.prev1[state], tr.prev0[state])
@@ -133,7 +145,7 @@ def viterbi(z: torch.Tensor, codebook: torch.Tensor, n_states: int):
         memb[:, t] = mem.to(torch.uint8)
         level[:, t] = (mem * N_SUBSETS + sub).to(torch.uint8)
         state = prev
-    return level, pathb, memb
+    return level, pathb, memb, end_state
 
 
 def _lloyd_under_trellis(codebook: torch.Tensor, z: torch.Tensor, n_states: int,

@@ -34,6 +34,8 @@ SIGNATURES: dict[str, tuple] = {
     "tp_subset_lut": (c_int, [c_int, POINTER(c_uint8), c_int]),
     "tp_device_delay": (c_int, [_I64, _P]),
     "tp_read_probe": (c_int, [_P, _I64, _P, _P]),
+    "tp_viterbi_workspace_bytes": (_I64, [_I64, _I64]),
+    "tp_tcq_viterbi": (c_int, [_P, _I64, _I64, _I64, _P, c_int, c_int, _P, _P, _P, _P, _P, _P, _I64, _P]),
     "tp_fwht_scale": (c_int, [_P, _P, _P, _I64, _I64, _I64, _P]),
     "tp_block_fwht_rows": (c_int, [_P, _P, _P, _P, _I64, _I64, _I64, _P]),
     "tp_window_decode_levels": (c_int, [_P, _I64, _P, _I64, _I64, _I64, c_int, c_int, _P, _I64, _P]),
