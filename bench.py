@@ -28,6 +28,9 @@ duration, timed with HIP events around back-to-back launches on the stream
 they run on.  ``read_reference`` is a plain streaming read of the step's
 byte count (``tp_read_probe``): the read bandwidth the box reaches with no
 compute, i.e. the practical ceiling the kernel is compared against.
+``encoder`` (comparison runs only) times the compress-time TCQ Viterbi
+search on a gate_proj-sized matrix; its CPU comparison sits in the
+CPU-baseline leg.
 ``cpu_baseline`` times the reference's CPU tiled path (the oracle's
 op-for-op restatement) on a bounded sample on this host.
 """
@@ -199,6 +202,48 @@ def read_reference(nbytes: int, reps: int = 20):
     return {"bytes_read": nbytes, "us": round(us, 2), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1)}
 
 
+def encoder_reference(rows: int = 9728, dim: int = 2560, cpu_rows: int = 256):
+    """Compress-time leg (not the headline): the TCQ Viterbi search
+    (tp_tcq_viterbi) over a Qwen3-4B gate_proj-sized matrix (k=3, S=64, the
+    stored trellis codebook).  Returns the figures and the first `cpu_rows`
+    rows with their GPU codes, which the CPU-baseline leg times and checks."""
+    from turbopress_amd.codebooks import default_codebook
+    from turbopress_amd.encoder import viterbi
+    gen = torch.Generator().manual_seed(0)
+    z = torch.randn(rows, dim, generator=gen)
+    cb = default_codebook(BITS, N_STATES).to(torch.float32)
+    zg = z.to("cuda")
+    viterbi(zg, cb, N_STATES)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 3
+    start.record()
+    for _ in range(reps):
+        out = viterbi(zg, cb, N_STATES)
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) / reps * 1e3
+    figures = {"rows": rows, "dim": dim, "bits": BITS, "n_states": N_STATES, "gpu_us": round(us, 1),
+               "gpu_weights_per_s": round(rows * dim / (us * 1e-6), 1)}
+    return figures, (z[:cpu_rows], cb, out[0][:cpu_rows].cpu(), rows)
+
+
+def cpu_encoder_baseline(sample) -> dict:
+    """The reference's fp32 Viterbi search restated on the CPU
+    (oracle.codebook_oracle.viterbi_full, torch) over the encoder leg's
+    sample rows, scaled to the whole matrix; also checks the GPU codes."""
+    from oracle.codebook_oracle import viterbi_full
+    z, cb, gpu_codes, rows = sample
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    t0 = time.perf_counter()
+    ref = viterbi_full(z, cb, N_STATES)
+    secs = time.perf_counter() - t0
+    return {"value": round(secs * rows / z.shape[0], 3), "unit": "s/matrix", "cores": threads, "kind": "port",
+            "sample": f"{z.shape[0]} of {rows} rows through the fp32 reference search (torch CPU), scaled",
+            "codes_match_gpu": bool(torch.equal(gpu_codes, ref[0]))}
+
+
 def cpu_baseline(budget_s: float):
     """The reference's CPU tiled path (oracle restatement), one Qwen3-4B layer
     at k=3, B=1, repeated until ~budget_s of CPU work, scaled to 36 layers."""
@@ -296,10 +341,18 @@ def main() -> int:
         log(f"device copy {args.copy_mib} MiB: {copy_ref['gbps']} GB/s (read + write)")
     read_ref = read_reference(nbytes)
     log(f"streaming read of {nbytes / 1e9:.4f} GB: {read_ref['us']} us, {read_ref['gbps']} GB/s")
+    enc, enc_sample = None, None
+    if not args.only_primary:
+        enc, enc_sample = encoder_reference()
+        log(f"TCQ Viterbi encoder, {enc['rows']}x{enc['dim']}: GPU {enc['gpu_us']} us")
     cpu = None
     if not args.no_cpu_baseline:
         log("CPU baseline")
         cpu = cpu_baseline(args.cpu_seconds)
+        if enc_sample is not None:
+            enc["cpu_baseline"] = cpu_encoder_baseline(enc_sample)
+            log(f"encoder CPU baseline (scaled): {enc['cpu_baseline']['value']} s, "
+                f"codes match GPU: {enc['cpu_baseline']['codes_match_gpu']}")
     gbps = nbytes / (ms * 1e-3) / 1e9
     gemv_bytes = nbytes - sum(2 * m.in_features for mods in layers for m in mods.values())
     gemv_gbps = gemv_bytes / (us_gemv * 1e-6) / 1e9
@@ -322,6 +375,7 @@ def main() -> int:
         "executors": extra,
         "copy_reference": copy_ref,
         "read_reference": read_ref,
+        "encoder": enc,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
