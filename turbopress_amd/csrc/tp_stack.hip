@@ -424,6 +424,7 @@ struct SlotEnv {
   const uint32_t* table;
   __amdgpu_buffer_rsrc_t zrs;   // the whole z buffer
   int total, batch, wave, lane, q, slot, bb, ordered, spin_limit, tid;
+  uint32_t tbase;  // blocks [0, tbase) are assigned by workgroup index, the rest by ticket
   uint32_t laneoff, pv, mv, slot_bit;
 };
 
@@ -613,7 +614,7 @@ __device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1
         __syncthreads();
         const int blk = __builtin_amdgcn_readfirstlane(s_tk[bseq & 1]);
         ++bseq;
-        if (E.tid == 0 && blk < E.total) pend = atomicAdd(&E.C->ticket, 1u);
+        if (E.tid == 0 && blk < E.total) pend = E.tbase + atomicAdd(&E.C->ticket, 1u);
         cur = nxt;
         nxt = stream_info(E, blk);
         lnext = false;  // the load cursor is in the new cur
@@ -673,16 +674,16 @@ tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
   E.zrs = buffer_rsrc(plan_rw + E.P.zbuf, (uint32_t)cread(E.P.info).zbuf_bytes);
   const uint32_t cb_lane = gld(codebook + (E.lane & ((2 << KB) - 1)));
 
-  if (E.tid == 0) {
-    s_tk[0] = (int)atomicAdd(&E.C->ticket, 1u);
-    s_tk[1] = (int)atomicAdd(&E.C->ticket, 1u);
-  }
+  // The first two blocks of every workgroup follow from its index, so the
+  // first weight loads need no ticket round trip; later blocks are claimed
+  // by ticket (offset by the 2 * grid blocks handed out this way).
+  E.tbase = 2u * gridDim.x;
+  const int blk0 = (int)blockIdx.x;
+  const int blk1 = (int)(blockIdx.x + gridDim.x);
+  uint32_t pend = 0;  // thread 0: ticket of the block after blk1
+  if (E.tid == 0) pend = E.tbase + atomicAdd(&E.C->ticket, 1u);
   build_pair_table_lanes<KB>(table, cb_lane, E.tid, kGroupThreads);
   __syncthreads();
-  const int blk0 = __builtin_amdgcn_readfirstlane(s_tk[0]);
-  const int blk1 = __builtin_amdgcn_readfirstlane(s_tk[1]);
-  uint32_t pend = 0;  // thread 0: ticket of the block after blk1
-  if (E.tid == 0) pend = atomicAdd(&E.C->ticket, 1u);
   // Register sets: 4 for 4 z columns per lane set (SB = 4), 2 for SB = 8
   // (four z loads per unit); 2 when a block is shorter than the pipeline.
   constexpr int DMAX = SB <= 4 ? kStreamDepth : 2;
