@@ -638,25 +638,44 @@ constexpr int kStreamDepth = 4;  // unit register sets of the stream (plans whos
 // unconditionally (after the last block, an in-range unit is reloaded and
 // never used), so the number of loads in flight is the same on every path
 // and each wait covers the oldest register set only.
+// What the host knows of a plan it initialised (lin_off == 0: nothing; the
+// kernel then reads and checks the plan header).
+struct PlanArgs {
+  int64_t lin_off;    // byte offset of the LinearDesc array from plan_ro
+  int64_t sched_off;  // byte offset of the launch's block schedule from plan_ro
+  int32_t total;      // blocks of the plan
+  int32_t batch;      // batch rows of the plan (<= SB)
+};
+
 template <int KB, int NS, int SB>
 __global__ void __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(4)))
 tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
-                      const uint16_t* __restrict__ codebook, int ordered, int spin_limit) {
+                      const uint16_t* __restrict__ codebook, int ordered, int spin_limit,
+                      PlanArgs pa) {
   __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
   __shared__ int s_tk[2];
   constexpr int MW = member_words(KB);
   SlotEnv E;
   E.P = stack_ro(plan_ro);
-  E.total = cread(E.P.info).total_blocks;
-  E.batch = cread(E.P.info).batch;
-  E.zbuf = plan_rw + E.P.zbuf;
   E.C = reinterpret_cast<StackCounters*>(plan_rw);
-  E.pdone = reinterpret_cast<uint32_t*>(plan_rw + E.P.pdone);
-  if (E.batch > SB || cread(E.P.info).n_rot <= 0) {  // not a plan for this kernel
-    if (threadIdx.x == 0 && blockIdx.x == 0) atomicExch(&E.C->error, 2u);
-    return;
+  if (pa.lin_off) {
+    // A plan the host set up and checked: the first block's schedule and
+    // descriptor loads do not wait for the plan header.
+    E.P.lin = reinterpret_cast<const LinearDesc*>(plan_ro + pa.lin_off);
+    E.sched = reinterpret_cast<const int32_t*>(plan_ro + pa.sched_off);
+    E.total = pa.total;
+    E.batch = pa.batch;
+  } else {
+    E.sched = ordered ? E.P.sched_o : E.P.sched_u;
+    E.total = cread(E.P.info).total_blocks;
+    E.batch = cread(E.P.info).batch;
+    if (E.batch > SB || cread(E.P.info).n_rot <= 0) {  // not a plan for this kernel
+      if (threadIdx.x == 0 && blockIdx.x == 0) atomicExch(&E.C->error, 2u);
+      return;
+    }
   }
-  E.sched = ordered ? E.P.sched_o : E.P.sched_u;
+  E.zbuf = plan_rw + E.P.zbuf;
+  E.pdone = reinterpret_cast<uint32_t*>(plan_rw + E.P.pdone);
   E.table = table;
   E.ordered = ordered;
   E.spin_limit = spin_limit;
@@ -674,14 +693,15 @@ tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
   E.zrs = buffer_rsrc(plan_rw + E.P.zbuf, (uint32_t)cread(E.P.info).zbuf_bytes);
   const uint32_t cb_lane = gld(codebook + (E.lane & ((2 << KB) - 1)));
 
-  // The first two blocks of every workgroup follow from its index, so the
-  // first weight loads need no ticket round trip; later blocks are claimed
-  // by ticket (offset by the 2 * grid blocks handed out this way).
-  E.tbase = 2u * gridDim.x;
+  // The first three blocks of every workgroup follow from its index: the
+  // first weight loads wait for no ticket, and the first ticket atomics
+  // happen at block ends, spread out in time, instead of all workgroups
+  // hitting the counter at once.  Later blocks are claimed by ticket (offset
+  // by the 3 * grid blocks handed out this way).
+  E.tbase = 3u * gridDim.x;
   const int blk0 = (int)blockIdx.x;
   const int blk1 = (int)(blockIdx.x + gridDim.x);
-  uint32_t pend = 0;  // thread 0: ticket of the block after blk1
-  if (E.tid == 0) pend = E.tbase + atomicAdd(&E.C->ticket, 1u);
+  uint32_t pend = blockIdx.x + 2u * gridDim.x;  // thread 0: the block after blk1
   build_pair_table_lanes<KB>(table, cb_lane, E.tid, kGroupThreads);
   __syncthreads();
   // Register sets: 4 for 4 z columns per lane set (SB = 4), 2 for SB = 8
@@ -861,6 +881,24 @@ inline int stack_z_rows(int64_t batch) { return batch <= 16 ? 16 : 32; }
 
 inline int slot_batch(int64_t batch) { return batch <= 4 ? 4 : 8; }
 
+// Each plan initialised in this process with a slot-kernel batch: its
+// rotation tile count, blocks, batch and layout offsets.  A plan the process
+// did not initialise gets kernels that read these from the plan header.
+struct PlanReg {
+  int n_rot, total, batch;
+  int64_t lin_off, sched_o_off, sched_u_off;
+};
+std::mutex g_plan_mutex;
+std::unordered_map<const void*, PlanReg> g_plans;
+
+inline bool plan_lookup(const void* plan, PlanReg* out) {
+  std::lock_guard<std::mutex> lock(g_plan_mutex);
+  const auto it = g_plans.find(plan);
+  if (it == g_plans.end()) return false;
+  *out = it->second;
+  return true;
+}
+
 template <int KB, int NS>
 int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t* cb, int ordered,
                 int spin_limit, hipStream_t s) {
@@ -870,12 +908,16 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
   const int grid = (int)(total_blocks < (int64_t)cus * per_cu ? total_blocks : (int64_t)cus * per_cu);
   if (batch <= kSlotMaxBatch) {
     const int sb = slot_batch(batch);
+    PlanArgs pa = {0, 0, 0, 0};
+    PlanReg reg;
+    if (plan_lookup(plan, &reg) && reg.batch == batch && reg.total == total_blocks)
+      pa = {reg.lin_off, ordered ? reg.sched_o_off : reg.sched_u_off, reg.total, reg.batch};
     if (sb == 4)
       hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 4>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
-                         ordered, spin_limit);
+                         ordered, spin_limit, pa);
     else
       hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 8>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
-                         ordered, spin_limit);
+                         ordered, spin_limit, pa);
   } else {
     const int zr = stack_z_rows(batch);
     const size_t zbytes = (size_t)zr * kZCols * 2;
@@ -889,16 +931,6 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
   return launch_status();
 }
 
-// Rotation tile count of each plan initialised in this process (a plan the
-// process did not initialise gets the kernel that reads the count itself).
-std::mutex g_plan_mutex;
-std::unordered_map<const void*, int> g_plan_rot;
-
-inline int plan_rotation_tiles(const void* plan) {
-  std::lock_guard<std::mutex> lock(g_plan_mutex);
-  const auto it = g_plan_rot.find(plan);
-  return it == g_plan_rot.end() ? 0 : it->second;
-}
 
 // Host-side sizes of a stack (validated); zbuf_bytes and n_rot are 0 for batch > 8.
 struct StackSizes {
@@ -1054,7 +1086,11 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
   }
   {
     std::lock_guard<std::mutex> lock(g_plan_mutex);
-    if (st == TP_OK && z.n_rot > 0) g_plan_rot[plan] = (int)z.n_rot; else g_plan_rot.erase(plan);
+    if (st == TP_OK && z.n_rot > 0)
+      g_plans[plan] = {(int)z.n_rot, (int)total, (int)batch, (int64_t)(lay.lin - kStackRO),
+                       (int64_t)(lay.sched_o - kStackRO), (int64_t)(lay.sched_u - kStackRO)};
+    else
+      g_plans.erase(plan);
   }
   free(host);
   return st;
@@ -1065,7 +1101,8 @@ extern "C" int tp_stack_rotate(void* plan, int64_t batch, void* stream) {
   if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
   if (batch > kSlotMaxBatch) return TP_OK;  // the LDS kernel rotates on the fly
   const char* ro = reinterpret_cast<const char*>(plan) + kStackRO;
-  const int n_rot = plan_rotation_tiles(plan);
+  PlanReg reg;
+  const int n_rot = plan_lookup(plan, &reg) ? reg.n_rot : 0;
   if (n_rot > 0)
     hipLaunchKernelGGL(tcq_stack_rotate_kernel<true>, dim3(n_rot), dim3(kRotThreads), 0, (hipStream_t)stream, ro);
   else
