@@ -1,0 +1,551 @@
+// One-pass decode-GEMV of one packed linear (or of 2..4 linears sharing one
+// input) at batch <= 8: the operator path of PackedTCQLinear.forward
+// (turbopress/runtime.py:304-334 -> triton_kernel.py:235-260 fwht_scale +
+// :132-157 packed_gemv), for calls that run one projection at a time.
+//
+// A single 9.4 MB linear has only ~1.5 units of work per wave of the chip, so
+// the launch is built around latency rather than streaming:
+//   * one workgroup of 16 waves per CU; the group owns `tpw` row tiles and
+//     splits each tile's K range into `s` chunks of at most 3 units, one
+//     chunk per wave, so every weight load of the launch is issued in the
+//     first few hundred cycles;
+//   * while those loads are in flight the workgroup builds the pair table
+//     and rotates the whole input into LDS (z = blockFWHT(x * rot_scale) /
+//     sqrt(block), fp32, rounded to fp16 once): every chunk then reads its B
+//     operands from LDS, and no second launch or global z buffer is needed;
+//   * the chunks of a tile are summed through LDS (no atomics, no workspace)
+//     and chunk 0's wave writes y = fp16(sum * scale) (+ bias).
+// The per-unit decode and MFMA step is the stack kernel's (tp_slot.h).
+#include "tp_slot.h"
+
+namespace tp {
+
+constexpr int kLinWaves = 16;
+constexpr int kLinThreads = 64 * kLinWaves;
+constexpr int kLinMaxUnits = 3;                      // units per wave, all loaded up front
+constexpr int kLinMaxParts = kMaxInlineLinears;
+constexpr int kLinRedBytes = kLinWaves * 64 * 16;    // one float4 per lane and wave
+
+struct LinPart {
+  const uint32_t* path;      // tiled path words [T][G][16][2]
+  const uint32_t* member;    // tiled member words [T][G][16][MW]
+  const uint16_t* x;         // first batch row of this launch
+  const uint16_t* rs;        // rot_scale [d]; null: x is z already (G4 * 256 columns, zero past d)
+  const uint16_t* scales;    // [n]
+  const uint16_t* bias;      // [n] or null
+  uint16_t* y;               // first batch row of this launch
+  int32_t n, T, ldx, ldy;
+  int32_t g0;                // first tile group of this linear
+  int32_t reserved;
+};
+
+struct LinArgs {
+  LinPart part[kLinMaxParts];
+  const uint16_t* codebook;
+  int32_t n_part, groups;    // tile groups over all linears
+  int32_t d, G4, hb, batch;  // batch: rows of this launch (<= SB)
+  int32_t c, s, tpw;         // units per chunk, chunks per tile, tiles per group
+  int32_t zstride;           // halves per staged z row (G4 * 256 + 8: rows start 4 banks apart)
+  float hdiv;                // sqrt(hb)
+};
+
+// Butterflies of one chunk (four columns per lane, lane-major) up to
+// distance min(hb, 256) / 2, then / sqrt(hb).
+__device__ __forceinline__ void lin_chunk_fwht(const LinArgs& a, int lane, float v[4]) {
+  const int hmax = a.hb < kChunkCols ? a.hb : kChunkCols;
+  if (hmax > 1) {
+    float p = v[0], q = v[1];
+    v[0] = p + q; v[1] = p - q;
+    p = v[2]; q = v[3];
+    v[2] = p + q; v[3] = p - q;
+  }
+  if (hmax > 2) {
+    float p = v[0], q = v[2];
+    v[0] = p + q; v[2] = p - q;
+    p = v[1]; q = v[3];
+    v[1] = p + q; v[3] = p - q;
+  }
+#pragma unroll
+  for (int sft = 0; sft < 6; ++sft) {
+    if ((4 << sft) < hmax) {
+      const bool upper = (lane >> sft) & 1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p = __shfl_xor(v[e], 1 << sft, 64);
+        v[e] = upper ? p - v[e] : v[e] + p;
+      }
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = v[e] / a.hdiv;
+}
+
+// z of one 256-column chunk of batch row b for Hadamard blocks <= 512, four
+// columns per lane: x * rs, (hb = 512: the signed sum of the block's two
+// chunks, i.e. the H_2 factor of H_512 = H_2 (x) H_256), the butterflies
+// inside the chunk, then / sqrt(hb).  Columns past d are zero.
+__device__ void lin_rotate_chunk(const LinArgs& a, const LinPart& P, int b, int cs, int lane, float v[4]) {
+  const uint16_t* xr = P.x + (size_t)b * P.ldx;
+  v[0] = v[1] = v[2] = v[3] = 0.f;
+  const int nsub = a.hb > kChunkCols ? a.hb / kChunkCols : 1;
+  const int base = a.hb > kChunkCols ? cs - cs % a.hb : cs;
+  const int o = a.hb > kChunkCols ? (cs % a.hb) / kChunkCols : 0;
+  for (int i = 0; i < nsub; ++i) {
+    const int c0 = base + i * kChunkCols + lane * 4;
+    if (c0 < a.d) {  // d is a multiple of 4: a lane's group is wholly inside or outside
+      float xv[4], rv[4];
+      load4h(xr + c0, xv);
+      load4h(P.rs + c0, rv);
+      const bool neg = __popc(i & o) & 1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] += neg ? -(xv[e] * rv[e]) : xv[e] * rv[e];
+    }
+  }
+  lin_chunk_fwht(a, lane, v);
+}
+
+// Activations of the first kLinPre staging items of a wave (item wave + 16k),
+// loaded at kernel start so that their latency overlaps the weight loads.
+// Blocks <= 512: item = (batch row, chunk), with the other chunk of a
+// 512-block; larger blocks: the chunks of batch row 0 (the first pass).
+constexpr int kLinPre = 2;
+struct XPre {
+  u32x2_t x[kLinPre][2], r[kLinPre][2];
+};
+
+__device__ __forceinline__ XPre lin_prefetch_x(const LinArgs& a, const LinPart& P, int wave, int lane) {
+  XPre f;
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(P.x, (uint32_t)((a.batch - 1) * P.ldx + a.d) * 2u);
+  const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(P.rs, (uint32_t)a.d * 2u);
+  const bool small = a.hb <= 2 * kChunkCols;
+  const int items = (small ? a.batch : 1) * a.G4;
+#pragma unroll
+  for (int k = 0; k < kLinPre; ++k) {
+    const int it = wave + kLinWaves * k;
+    const bool ok = it < items;
+    const int b = ok ? it / a.G4 : 0;
+    const int cs = (ok ? it - b * a.G4 : 0) * kChunkCols;
+    const int base = (small && a.hb > kChunkCols) ? cs - cs % a.hb : cs;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c0 = base + i * kChunkCols + lane * 4;
+      const bool in = ok && (i == 0 || (small && a.hb > kChunkCols)) && c0 < a.d;
+      f.x[k][i] = __builtin_amdgcn_raw_buffer_load_b64(xrs, in ? (uint32_t)(b * P.ldx + c0) * 2u : kOutOfRange, 0, 0);
+      f.r[k][i] = __builtin_amdgcn_raw_buffer_load_b64(rrs, in ? (uint32_t)c0 * 2u : kOutOfRange, 0, 0);
+    }
+  }
+  return f;
+}
+
+// x * rs of prefetched item k (the signed sum of both chunks of a 512-block).
+__device__ __forceinline__ void lin_pre_product(const LinArgs& a, const XPre& f, int k, int cs, float v[4]) {
+  float xv[4], rv[4];
+  unpack4h(uint2{f.x[k][0][0], f.x[k][0][1]}, xv);
+  unpack4h(uint2{f.r[k][0][0], f.r[k][0][1]}, rv);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = 0.f + xv[e] * rv[e];
+  if (a.hb > kChunkCols && a.hb <= 2 * kChunkCols) {
+    const bool neg = (cs % a.hb) != 0;  // second chunk of the block: row 1 of H_2
+    unpack4h(uint2{f.x[k][1][0], f.x[k][1][1]}, xv);
+    unpack4h(uint2{f.r[k][1][0], f.r[k][1][1]}, rv);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += neg ? -(xv[e] * rv[e]) : xv[e] * rv[e];
+  }
+}
+
+__device__ __forceinline__ void store4h(uint16_t* p, const float v[4]) {
+  u32x2_t w = {(uint32_t)f2h(v[0]) | ((uint32_t)f2h(v[1]) << 16), (uint32_t)f2h(v[2]) | ((uint32_t)f2h(v[3]) << 16)};
+  *reinterpret_cast<u32x2_t*>(p) = w;
+}
+
+// Stage z rows [0, batch) x columns [0, G4 * 256) of linear P in LDS.
+// Blocks of 1024..4096 columns (d a multiple of 1024, so G4 * 256 == d) go
+// through `scr` one batch row at a time: H_256 inside every chunk (fp32),
+// then H_(hb/256) across the chunks of each block -- the stages in order of
+// distance, as the reference's transform runs them.
+template <bool ROT>
+__device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre& f, bool pre, uint16_t* zl, float* scr,
+                            int tid, int wave, int lane) {
+  const int nch = a.G4;
+  if constexpr (!ROT) {
+    const int per_row = nch * kChunkCols / 8;
+    for (int i = tid; i < a.batch * per_row; i += kLinThreads) {
+      const int b = i / per_row, c8 = (i - b * per_row) * 8;
+      *reinterpret_cast<u32x4_t*>(zl + b * a.zstride + c8) =
+          *(const TP_GLOBAL u32x4_t*)(P.x + (size_t)b * P.ldx + c8);
+    }
+    return;
+  }
+  if (a.hb <= 2 * kChunkCols) {
+    int it0 = wave;
+    if (pre) {
+#pragma unroll
+      for (int k = 0; k < kLinPre; ++k) {
+        const int it = wave + kLinWaves * k;
+        if (it < a.batch * nch) {
+          const int b = it / nch, ci = it - b * nch;
+          float v[4];
+          lin_pre_product(a, f, k, ci * kChunkCols, v);
+          lin_chunk_fwht(a, lane, v);
+          store4h(zl + b * a.zstride + ci * kChunkCols + lane * 4, v);
+        }
+      }
+      it0 = wave + kLinWaves * kLinPre;
+    }
+    for (int it = it0; it < a.batch * nch; it += kLinWaves) {
+      const int b = it / nch, ci = it - b * nch;
+      float v[4];
+      lin_rotate_chunk(a, P, b, ci * kChunkCols, lane, v);
+      store4h(zl + b * a.zstride + ci * kChunkCols + lane * 4, v);
+    }
+    return;
+  }
+  const int m = a.hb / kChunkCols;  // 4, 8 or 16
+  for (int b = 0; b < a.batch; ++b) {
+    const uint16_t* xr = P.x + (size_t)b * P.ldx;
+    for (int ci = wave; ci < nch; ci += kLinWaves) {
+      const int c0 = ci * kChunkCols + lane * 4;
+      const int k = (ci - wave) / kLinWaves;  // prefetched item of row 0
+      float v[4];
+      if (pre && b == 0 && k < kLinPre) {
+        // (k < kLinPre is uniform: select the registers without indexing)
+        float t[4];
+#pragma unroll
+        for (int kk = 0; kk < kLinPre; ++kk) {
+          if (kk == k) {
+            lin_pre_product(a, f, kk, ci * kChunkCols, t);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = t[e];
+          }
+        }
+      } else {
+        float xv[4], rv[4];
+        load4h(xr + c0, xv);
+        load4h(P.rs + c0, rv);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = xv[e] * rv[e];
+      }
+      float p = v[0], q = v[1];
+      v[0] = p + q; v[1] = p - q;
+      p = v[2]; q = v[3];
+      v[2] = p + q; v[3] = p - q;
+      p = v[0]; q = v[2];
+      v[0] = p + q; v[2] = p - q;
+      p = v[1]; q = v[3];
+      v[1] = p + q; v[3] = p - q;
+#pragma unroll
+      for (int sft = 0; sft < 6; ++sft) {
+        const bool upper = (lane >> sft) & 1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float t = __shfl_xor(v[e], 1 << sft, 64);
+          v[e] = upper ? t - v[e] : v[e] + t;
+        }
+      }
+      *reinterpret_cast<float4_t*>(scr + c0) = float4_t{v[0], v[1], v[2], v[3]};
+    }
+    __syncthreads();
+    const int items = a.d / m;  // (block, position inside the chunk) pairs
+    for (int it = tid; it < items; it += kLinThreads) {
+      const int h = it / kChunkCols, pos = it - h * kChunkCols;
+      const int base = h * a.hb + pos;
+      float u[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) u[i] = i < m ? scr[base + i * kChunkCols] : 0.f;
+#pragma unroll
+      for (int dist = 1; dist < 16; dist <<= 1) {
+        if (dist < m) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            if (!(i & dist)) {
+              const float p = u[i], q = u[i + dist];
+              u[i] = p + q;
+              u[i + dist] = p - q;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        if (i < m) zl[b * a.zstride + base + i * kChunkCols] = f2h(u[i] / a.hdiv);
+    }
+    __syncthreads();
+  }
+}
+
+// MULTI: 2..4 linears (part of a group is found per tile group); otherwise
+// one linear, whose argument fields sit at fixed offsets and load at once.
+template <int KB, int NS, int SB, bool ROT, bool MULTI>
+__global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a) {
+  __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
+  extern __shared__ __attribute__((aligned(16))) char lin_lds[];
+  constexpr int MW = member_words(KB);
+  constexpr int SLOTS = 16 / SB;
+  constexpr int NZ = 8 / SLOTS;
+  constexpr uint32_t unit_p = 4u * kTileRows * 8u;       // path bytes per unit of a tile
+  constexpr uint32_t unit_m = 4u * kTileRows * MW * 4u;  // member bytes per unit of a tile
+  uint16_t* zl = reinterpret_cast<uint16_t*>(lin_lds);
+  float* scr = reinterpret_cast<float*>(lin_lds + (((size_t)a.batch * a.zstride * 2 + 15) & ~(size_t)15));
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int slot = r / SB, bb = r % SB;
+  const uint32_t slot_bit = 1u << slot;
+  const uint32_t laneoff = lane_offsets<KB>(lane);
+  const uint32_t pv = (uint32_t)(q * kTileRows + r) * 8u;
+  const uint32_t mv = (uint32_t)(q * kTileRows + r) * MW * 4u;
+  const uint32_t cb_lane = gld(a.codebook + (lane & ((2 << KB) - 1)));
+  // B operand halves of this lane inside a unit's staged z (rows past the
+  // batch read row 0: their MFMA columns are never written out).
+  const int bbz = bb < a.batch ? bb : 0;
+  int zoff[NZ];
+#pragma unroll
+  for (int l = 0; l < NZ; ++l) zoff[l] = bbz * a.zstride + q * kSegCols + mfma_col(l * SLOTS + slot);
+  const int lt = wave / a.s;        // local tile of this wave
+  const int j = wave - lt * a.s;    // K chunk of this wave
+  const int u0 = j * a.c;
+  const int nu = min(a.c, a.G4 - u0);
+  const uint32_t tile_p = (uint32_t)a.G4 * unit_p;  // path bytes of one tile
+  const uint32_t tile_m = (uint32_t)a.G4 * unit_m;  // member bytes of one tile
+  int staged = -1;
+
+  for (int g = blockIdx.x; g < a.groups; g += gridDim.x) {
+    int p = 0;
+    LinPart P = a.part[0];
+    if constexpr (MULTI) {
+#pragma unroll
+      for (int i = 1; i < kLinMaxParts; ++i)
+        if (i < a.n_part && g >= a.part[i].g0) p = i;
+#pragma unroll
+      for (int i = 1; i < kLinMaxParts; ++i)
+        if (p == i) P = a.part[i];
+    }
+    const int t = (g - P.g0) * a.tpw + lt;
+    const bool active = lt < a.tpw && t < P.T && nu > 0;  // wave-uniform
+    const int tt = active ? t : 0;
+    // The first group's activations load before its weights (they gate the
+    // rotation, which every decode waits for).
+    const bool pre = ROT && p != staged && g == (int)blockIdx.x;
+    XPre xf;
+    if constexpr (ROT) {
+      if (pre) xf = lin_prefetch_x(a, P, wave, lane);
+    }
+
+    // Every weight load of this wave, then the halo word (path word 1 of
+    // the unit before the chunk, K block 3 lanes) and the row scales.
+    const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(reinterpret_cast<const char*>(P.path) + (size_t)tt * tile_p, tile_p);
+    const __amdgpu_buffer_rsrc_t mrs = buffer_rsrc(reinterpret_cast<const char*>(P.member) + (size_t)tt * tile_m, tile_m);
+    UnitRegs<MW, NZ> R[kLinMaxUnits];
+#pragma unroll
+    for (int u = 0; u < kLinMaxUnits; ++u) {
+      const bool ok = active && u < nu;
+      const uint32_t gu = (uint32_t)(ok ? u0 + u : 0);
+      R[u].X = __builtin_amdgcn_raw_buffer_load_b64(prs, ok ? pv : kOutOfRange, gu * unit_p, 0);
+      R[u].M = MemberBuf<MW>::load(mrs, ok ? mv : kOutOfRange, gu * unit_m);
+    }
+    const uint32_t x1_prev = __builtin_amdgcn_raw_buffer_load_b32(
+        prs, (active && u0 > 0) ? pv + 4u : kOutOfRange, (uint32_t)(u0 > 0 ? u0 - 1 : 0) * unit_p, 0);
+    const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(P.scales, (uint32_t)P.n * 2u);
+    uint32_t sc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      sc[i] = __builtin_amdgcn_raw_buffer_load_b16(srs, (uint32_t)(tt * kTileRows + 4 * q + i) * 2u, 0, 0);
+
+    if (g == (int)blockIdx.x) build_pair_table_lanes<KB>(table, cb_lane, tid, kLinThreads);
+    if (p != staged) {
+      if (staged >= 0) __syncthreads();  // the previous group's reads of z and scr are done
+      lin_stage_z<ROT>(a, P, xf, pre, zl, scr, tid, wave, lane);
+      staged = p;
+    }
+    __syncthreads();
+
+    if (active) {
+      float4_t acc[SLOTS];
+#pragma unroll
+      for (int s = 0; s < SLOTS; ++s) acc[s] = float4_t{0.f, 0.f, 0.f, 0.f};
+      uint32_t prev = x1_prev;
+#pragma unroll
+      for (int u = 0; u < kLinMaxUnits; ++u) {
+        if (u < nu) {
+          const int cbase = (u0 + u) * kChunkCols;
+#pragma unroll
+          for (int l = 0; l < NZ; ++l) R[u].Z[l] = *reinterpret_cast<const u32x4_t*>(zl + zoff[l] + cbase);
+          const uint32_t provide = (q == 3) ? prev : R[u].X[1];
+          slot_unit<KB, NS, SB, MW, NZ>(R[u], provide, lane, laneoff, table, acc);
+          prev = R[u].X[1];
+        }
+      }
+      // accumulator `slot` holds this lane's column; sum the slots of each batch row
+      float4_t v = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < SLOTS; ++s) {
+        const float msk = (float)__builtin_amdgcn_ubfe(slot_bit, (uint32_t)s, 1u);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(acc[s][i], msk, v[i]);
+      }
+#pragma unroll
+      for (int w = SB; w < 16; w <<= 1)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], w, 64);
+      *reinterpret_cast<float4_t*>(scr + (wave * 64 + lane) * 4) = v;
+    }
+    __syncthreads();
+    if (active && j == 0) {
+      float4_t v = *reinterpret_cast<const float4_t*>(scr + (wave * 64 + lane) * 4);
+      for (int k = 1; k < a.s; ++k) {
+        const float4_t w = *reinterpret_cast<const float4_t*>(scr + ((wave + k) * 64 + lane) * 4);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] += w[i];
+      }
+      if (slot == 0 && bb < a.batch) {
+        const int row0 = t * kTileRows + 4 * q;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = row0 + i;
+          if (row >= P.n) continue;
+          uint16_t out = f2h(v[i] * h2f((uint16_t)sc[i]));
+          if (P.bias) out = f2h(h2f(out) + h2f(gld(P.bias + row)));
+          gst(P.y + (size_t)bb * P.ldy + row, out);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+namespace {
+
+// Largest LDS allocation of one workgroup on the current device (cached).
+int device_max_lds() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
+  if (!cached[dev]) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+      v = 64 * 1024;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}
+
+template <int KB, int NS, int SB, bool ROT>
+void launch_linear(const LinArgs& a, int grid, size_t dyn, hipStream_t s) {
+  auto kern = a.n_part > 1 ? tcq_linear_kernel<KB, NS, SB, ROT, true> : tcq_linear_kernel<KB, NS, SB, ROT, false>;
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)dyn);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kLinThreads), dyn, s, a);
+}
+
+template <int KB, int NS>
+void launch_linear_sb(const LinArgs& a, int grid, size_t dyn, bool rot, hipStream_t s) {
+  if (a.batch <= 4)
+    rot ? launch_linear<KB, NS, 4, true>(a, grid, dyn, s) : launch_linear<KB, NS, 4, false>(a, grid, dyn, s);
+  else
+    rot ? launch_linear<KB, NS, 8, true>(a, grid, dyn, s) : launch_linear<KB, NS, 8, false>(a, grid, dyn, s);
+}
+
+}  // namespace
+
+int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
+                        int bits, int n_states, hipStream_t s) {
+  if (batch < 1 || batch > 8 || n_lin < 1 || n_lin > kLinMaxParts) return kLinearNotHandled;
+  if (bits != 2 && bits != 3) return kLinearNotHandled;
+  const bool rot = ls[0].rot_scale != nullptr;
+  const int64_t d = ls[0].d, hb = rot ? ls[0].block : 1;
+  for (int i = 1; i < n_lin; ++i)
+    if (ls[i].d != d || (rot && ls[i].block != hb) || ls[i].x != ls[0].x || ls[i].ldx != ls[0].ldx)
+      return kLinearNotHandled;
+  if (rot && hb > 4096) return kLinearNotHandled;
+  Geom g0;
+  if (tiled_geom(ls[0].n, d, bits, &g0) != TP_OK) return kLinearNotHandled;
+  const int64_t G4 = g0.G4;
+  if (G4 > (int64_t)kLinWaves * kLinMaxUnits) return kLinearNotHandled;
+  if (rot && hb > 2 * kChunkCols && G4 * kChunkCols != d) return kLinearNotHandled;
+  // Staging issues the activations of two items per wave ahead of the
+  // weights; each further item costs a dependent round trip, so larger
+  // inputs (batch * 256-column chunks) keep the split-K kernel.
+  if (batch * G4 > (int64_t)kLinWaves * (kLinPre + 1) || batch > 4) return kLinearNotHandled;
+
+  // LDS: 64 KiB table (static) + z rows + max(partial sums, one fp32 row).
+  const int64_t zstride = G4 * kChunkCols + 8;
+  const int64_t scr = std::max<int64_t>(kLinRedBytes, (rot && hb > 2 * kChunkCols) ? d * 4 : 0);
+  const int64_t room = (int64_t)device_max_lds() - kTableBytes - scr - 16;
+  const int64_t rows_fit = room > 0 ? room / (zstride * 2) : 0;
+  if (rows_fit < batch) return kLinearNotHandled;  // one launch for all rows (no weight re-reads)
+
+  // Split of each tile's K range: chunks of c units, s chunks per tile, tpw
+  // tiles per group of 16 waves; c grows until the groups fit one per CU.
+  int64_t T[kLinMaxParts];
+  for (int i = 0; i < n_lin; ++i) {
+    Geom g;
+    if (tiled_geom(ls[i].n, d, bits, &g) != TP_OK) return kLinearNotHandled;
+    T[i] = g.T;
+  }
+  const int cus = device_cu_count();
+  int64_t c = (G4 + kLinWaves - 1) / kLinWaves, sc = 0, tpw = 0, groups = 0;
+  for (;; ++c) {
+    sc = (G4 + c - 1) / c;
+    tpw = kLinWaves / sc;
+    groups = 0;
+    for (int i = 0; i < n_lin; ++i) groups += (T[i] + tpw - 1) / tpw;
+    if (groups <= cus || c >= kLinMaxUnits) break;
+  }
+  if (groups > INT32_MAX / 2) return kLinearNotHandled;
+
+  LinArgs a;
+  a.codebook = codebook;
+  a.n_part = n_lin;
+  a.groups = (int32_t)groups;
+  a.d = (int32_t)d;
+  a.G4 = (int32_t)G4;
+  a.hb = (int32_t)hb;
+  a.c = (int32_t)c;
+  a.s = (int32_t)sc;
+  a.tpw = (int32_t)tpw;
+  a.zstride = (int32_t)zstride;
+  a.hdiv = (float)__builtin_sqrt((double)hb);
+  int64_t g0acc = 0;
+  for (int i = 0; i < kLinMaxParts; ++i) {
+    const TiledLinearArgs& l = ls[i < n_lin ? i : 0];
+    LinPart& P = a.part[i];
+    P.path = reinterpret_cast<const uint32_t*>(l.path_tiled);
+    P.member = reinterpret_cast<const uint32_t*>(l.member_tiled);
+    P.rs = rot ? l.rot_scale : nullptr;
+    P.scales = l.scales;
+    P.bias = l.bias;
+    P.n = (int32_t)l.n;
+    P.T = (int32_t)T[i < n_lin ? i : 0];
+    P.ldx = (int32_t)l.ldx;
+    P.ldy = (int32_t)l.ldy;
+    P.g0 = (int32_t)(i < n_lin ? g0acc : groups);
+    P.reserved = 0;
+    if (i < n_lin) g0acc += (T[i] + tpw - 1) / tpw;
+  }
+  const int grid = (int)std::min<int64_t>(groups, cus);
+  a.batch = (int32_t)batch;
+  for (int i = 0; i < kLinMaxParts; ++i) {
+    const TiledLinearArgs& l = ls[i < n_lin ? i : 0];
+    a.part[i].x = l.x;
+    a.part[i].y = l.y;
+  }
+  const size_t dyn = (size_t)((batch * zstride * 2 + 15) & ~(int64_t)15) + (size_t)scr;
+  switch (bits * 100 + n_states) {
+    case 204: launch_linear_sb<2, 4>(a, grid, dyn, rot, s); break;
+    case 208: launch_linear_sb<2, 8>(a, grid, dyn, rot, s); break;
+    case 216: launch_linear_sb<2, 16>(a, grid, dyn, rot, s); break;
+    case 264: launch_linear_sb<2, 64>(a, grid, dyn, rot, s); break;
+    case 304: launch_linear_sb<3, 4>(a, grid, dyn, rot, s); break;
+    case 308: launch_linear_sb<3, 8>(a, grid, dyn, rot, s); break;
+    case 316: launch_linear_sb<3, 16>(a, grid, dyn, rot, s); break;
+    case 364: launch_linear_sb<3, 64>(a, grid, dyn, rot, s); break;
+    default: return TP_ERR_UNSUPPORTED_STATES;
+  }
+  return launch_status();
+}
+
+}  // namespace tp

@@ -32,6 +32,7 @@
 // Batch 9..32 runs tcq_stack_lds_kernel: the workgroup rotates each
 // 512-column chunk of x into LDS and all waves read it as B operands.
 #include "tp_tiled_common.h"
+#include "tp_slot.h"
 
 #include <algorithm>
 #include <mutex>
@@ -191,12 +192,6 @@ __device__ inline void wait_phase(const StackRO& P, uint32_t* pdone, StackCounte
 // sqrt(block)), all in fp32, z rounded to fp16 once.  A block larger than
 // 4096 (H_hb = H_(hb/4096) (x) H_4096) first sums its 4096-column sub-tiles
 // with the signs of the tile's row of H_(hb/4096).
-constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format
-constexpr uint32_t kOutOfRange = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferFlags);
-}
 
 constexpr int kRotTile = 4096;
 constexpr int kRotThreads = 256;
@@ -338,81 +333,6 @@ tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
 // ---------------------------------------------------------------------------
 // 2. slot kernel (batch <= 8)
 // ---------------------------------------------------------------------------
-
-__device__ __forceinline__ u32x2_t gld2v(const char* p) { return *(const TP_GLOBAL u32x2_t*)p; }
-
-template <int MW> struct MemberBuf;
-template <> struct MemberBuf<2> {
-  typedef u32x2_t type;
-  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
-    return __builtin_amdgcn_raw_buffer_load_b64(r, v, s, 0);
-  }
-};
-template <> struct MemberBuf<4> {
-  typedef u32x4_t type;
-  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, v, s, 0);
-  }
-};
-
-template <int MW> struct MemberLoad;
-template <> struct MemberLoad<2> {
-  typedef u32x2_t type;
-  static __device__ __forceinline__ type load(const char* p) { return *(const TP_GLOBAL u32x2_t*)p; }
-};
-template <> struct MemberLoad<4> {
-  typedef u32x4_t type;
-  static __device__ __forceinline__ type load(const char* p) { return *(const TP_GLOBAL u32x4_t*)p; }
-};
-
-// Loads of one unit of one lane.
-template <int MW, int NZ>
-struct UnitRegs {
-  u32x2_t X;
-  typename MemberBuf<MW>::type M;
-  u32x4_t Z[NZ];
-};
-
-// Column (inside a 64-column segment) of the first of the 8 K positions of
-// MFMA i of a unit: word x = i / 4 holds columns 16x..16x+15 and
-// 32+16x..32+16x+15; MFMA j = i % 4 takes 8 of them.
-__host__ __device__ constexpr int mfma_col(int i) {
-  return 16 * (i >> 2) + ((i & 2) ? 32 : 0) + ((i & 1) ? 8 : 0);
-}
-
-// One unit of one wave: decode 64 weights per lane, 8 MFMAs.  Word 1 is
-// decoded first: its previous word is this lane's word 0, so the halo
-// exchange needed by word 0 completes meanwhile.
-template <int KB, int NS, int SB, int MW, int NZ>
-__device__ __forceinline__ void slot_unit(const UnitRegs<MW, NZ>& g, const uint32_t provide, const int lane,
-                                          const uint32_t laneoff, const uint32_t* table, float4_t* acc) {
-  constexpr int SLOTS = 16 / SB;
-  const uint32_t halo = (uint32_t)__shfl((int)provide, (lane + 48) & 63, 64);
-  MemberWords<KB> m[2];
-  if constexpr (KB == 3) {
-    m[0].a = g.M[0]; m[0].b = g.M[1]; m[1].a = g.M[2]; m[1].b = g.M[3];
-  } else {
-    m[0].w = g.M[0]; m[1].w = g.M[1];
-  }
-#pragma unroll
-  for (int xi = 0; xi < 2; ++xi) {
-    const int x = 1 - xi;
-    u32x4_t A[4];
-    if (x == 1) {
-      decode_word<KB, NS>(g.X[1], g.X[0], m[1], table, laneoff, A);
-    } else {
-      const uint32_t P = ((halo >> 1) & 0x55555555u) | ((g.X[1] << 1) & 0xAAAAAAAAu);
-      decode_word<KB, NS>(g.X[0], P, m[0], table, laneoff, A);
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = 4 * x + j;
-      const half8_t b = __builtin_bit_cast(half8_t, g.Z[i / SLOTS]);
-      acc[i % SLOTS] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, A[j]), b,
-                                                             acc[i % SLOTS], 0, 0, 0);
-    }
-  }
-}
 
 // Read-only state of one wave of the slot kernel.
 struct SlotEnv {

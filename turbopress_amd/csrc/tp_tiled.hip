@@ -411,22 +411,6 @@ extern "C" int tp_decode_tiled(const uint8_t* path_tiled, const uint8_t* member_
 
 namespace tp {
 
-struct TiledLinearArgs {
-  const uint8_t* path_tiled;
-  const uint8_t* member_tiled;
-  const uint16_t* x;     // rotated z (rot_scale == null) or raw activations (fused rotation)
-  int64_t ldx;
-  const uint16_t* rot_scale;
-  int64_t block;         // Hadamard block (fused rotation)
-  const uint16_t* scales;
-  const uint16_t* bias;
-  uint16_t* y;
-  int64_t ldy;
-  int64_t n, d;
-  void* workspace;
-  int64_t workspace_bytes;
-};
-
 // Dynamic LDS (z staging); the 64 KiB pair table is static.
 constexpr size_t gemv_lds_bytes(int nbt) {
   return (size_t)16 * nbt * kZCols * 2;
@@ -526,6 +510,9 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
   }
   for (int i = n_lin; i < kMaxInlineLinears; ++i) a.lin[i] = a.lin[0];
   if (total_blocks > INT32_MAX) return TP_ERR_BAD_DIMS;
+  // Batch <= 8 runs the one-pass kernel (tp_linear.hip) when it applies.
+  const int fast = linear_forward_fast(ls, n_lin, batch, codebook, bits, n_states, (hipStream_t)stream);
+  if (fast != kLinearNotHandled) return fast;
   a.total_blocks = (int32_t)total_blocks;
   const int wg_per_cu = nbt == 1 ? 2 : 1;
   int grid = (int)(total_blocks < (int64_t)cus * wg_per_cu ? total_blocks : (int64_t)cus * wg_per_cu);

@@ -444,6 +444,30 @@ __device__ void stage_z(const LinearDesc& L, int gu0, int ngu, int batch, uint16
   }
 }
 
+// One linear of a host-side launch (rotation fused when rot_scale is set).
+struct TiledLinearArgs {
+  const uint8_t* path_tiled;
+  const uint8_t* member_tiled;
+  const uint16_t* x;     // rotated z (rot_scale == null) or raw activations (fused rotation)
+  int64_t ldx;
+  const uint16_t* rot_scale;
+  int64_t block;         // Hadamard block (fused rotation)
+  const uint16_t* scales;
+  const uint16_t* bias;
+  uint16_t* y;
+  int64_t ldy;
+  int64_t n, d;
+  void* workspace;
+  int64_t workspace_bytes;
+};
+
+// Batch <= 8 decode-GEMV of 1..4 linears on one input in one pass
+// (tp_linear.hip), for arguments the caller has validated.  Returns a status,
+// or kLinearNotHandled when the shapes need the split-K kernel instead.
+constexpr int kLinearNotHandled = 1 << 20;
+int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
+                        int bits, int n_states, hipStream_t s);
+
 // ---------------------------------------------------------------------------
 // host-side geometry
 // ---------------------------------------------------------------------------
