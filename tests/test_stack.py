@@ -63,6 +63,16 @@ def test_stack_k2_and_repeat_runs_reset_counters(cuda):
     _check(payloads, stack)
 
 
+@pytest.mark.parametrize("batch", [1, 4, 8, 12])
+def test_stack_k4(cuda, batch):
+    """4 bits/weight: slot kernel (batch <= 8) and LDS-staged kernel."""
+    payloads, stack = _build(cuda, MIXED, batch, bits=4, bias=True)
+    stack.run()
+    torch.cuda.synchronize()
+    _check(payloads, stack)
+    assert stack.error() == 0
+
+
 def test_stack_graph_replay_with_new_inputs(cuda):
     payloads, stack = _build(cuda, [(d, n, ph) for (d, n), ph in
                                     zip(QWEN3_4B_LAYER.values(), (0, 0, 0, 1, 2, 2, 3))], 1, ordered=True)

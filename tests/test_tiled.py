@@ -24,6 +24,7 @@ GEMV_TOL = 2e-3
 DECODE_CASES = [
     (16, 64, 3, 64), (17, 64, 2, 64), (33, 576, 2, 64), (40, 1000, 3, 64),
     (5, 200, 3, 16), (31, 328, 2, 8), (20, 130, 3, 4), (48, 2560, 3, 64), (64, 9728, 2, 64),
+    (16, 64, 4, 64), (33, 576, 4, 64), (40, 1000, 4, 16), (20, 130, 4, 4), (31, 328, 4, 8), (48, 2560, 4, 64),
 ]
 
 
@@ -58,6 +59,11 @@ GEMV_CASES = [
     (9728, 2560, 2, 64, 32),
     (300, 512, 3, 8, 40),
     (2560, 4096, 3, 64, 4),
+    (9728, 2560, 4, 64, 1),      # k=4: one-pass kernel
+    (2560, 9728, 4, 64, 3),
+    (130, 200, 4, 16, 2),
+    (1024, 2560, 4, 64, 8),      # k=4: split-K kernel
+    (300, 512, 4, 8, 20),        # k=4: LDS-staged batches
 ]
 
 
@@ -126,7 +132,7 @@ def test_graph_replays_match_eager(cuda):
 
 FUSED_CASES = [  # (n, d, bits): Hadamard block d & -d = 2, 4, 64, 512, 1024, 2048, 4096
     (40, 130, 3), (48, 100, 2), (1536, 576, 2), (256, 2560, 3), (200, 3072, 3),
-    (300, 2048, 2), (2560, 4096, 3),
+    (300, 2048, 2), (2560, 4096, 3), (1536, 576, 4), (256, 2560, 4), (200, 3072, 4), (2560, 4096, 4),
 ]
 
 

@@ -109,18 +109,22 @@ __device__ void lin_rotate_chunk(const LinArgs& a, const LinPart& P, int b, int 
 // Blocks <= 512: item = (batch row, chunk), with the other chunk of a
 // 512-block; larger blocks: the chunks of batch row 0 (the first pass).
 constexpr int kLinPre = 2;
+// (k=4 keeps one: its member words take the registers of the other)
+__host__ __device__ constexpr int lin_pre(int bits) { return bits == 4 ? 1 : kLinPre; }
+template <int NPRE>
 struct XPre {
-  u32x2_t x[kLinPre][2], r[kLinPre][2];
+  u32x2_t x[NPRE][2], r[NPRE][2];
 };
 
-__device__ __forceinline__ XPre lin_prefetch_x(const LinArgs& a, const LinPart& P, int wave, int lane) {
-  XPre f;
+template <int NPRE>
+__device__ __forceinline__ XPre<NPRE> lin_prefetch_x(const LinArgs& a, const LinPart& P, int wave, int lane) {
+  XPre<NPRE> f;
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(P.x, (uint32_t)((a.batch - 1) * P.ldx + a.d) * 2u);
   const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(P.rs, (uint32_t)a.d * 2u);
   const bool small = a.hb <= 2 * kChunkCols;
   const int items = (small ? a.batch : 1) * a.G4;
 #pragma unroll
-  for (int k = 0; k < kLinPre; ++k) {
+  for (int k = 0; k < NPRE; ++k) {
     const int it = wave + kLinWaves * k;
     const bool ok = it < items;
     const int b = ok ? it / a.G4 : 0;
@@ -138,7 +142,8 @@ __device__ __forceinline__ XPre lin_prefetch_x(const LinArgs& a, const LinPart& 
 }
 
 // x * rs of prefetched item k (the signed sum of both chunks of a 512-block).
-__device__ __forceinline__ void lin_pre_product(const LinArgs& a, const XPre& f, int k, int cs, float v[4]) {
+template <int NPRE>
+__device__ __forceinline__ void lin_pre_product(const LinArgs& a, const XPre<NPRE>& f, int k, int cs, float v[4]) {
   float xv[4], rv[4];
   unpack4h(uint2{f.x[k][0][0], f.x[k][0][1]}, xv);
   unpack4h(uint2{f.r[k][0][0], f.r[k][0][1]}, rv);
@@ -163,8 +168,8 @@ __device__ __forceinline__ void store4h(uint16_t* p, const float v[4]) {
 // through `scr` one batch row at a time: H_256 inside every chunk (fp32),
 // then H_(hb/256) across the chunks of each block -- the stages in order of
 // distance, as the reference's transform runs them.
-template <bool ROT>
-__device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre& f, bool pre, uint16_t* zl, float* scr,
+template <bool ROT, int NPRE>
+__device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>& f, bool pre, uint16_t* zl, float* scr,
                             int tid, int wave, int lane) {
   const int nch = a.G4;
   if constexpr (!ROT) {
@@ -180,7 +185,7 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre& f, b
     int it0 = wave;
     if (pre) {
 #pragma unroll
-      for (int k = 0; k < kLinPre; ++k) {
+      for (int k = 0; k < NPRE; ++k) {
         const int it = wave + kLinWaves * k;
         if (it < a.batch * nch) {
           const int b = it / nch, ci = it - b * nch;
@@ -190,7 +195,7 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre& f, b
           store4h(zl + b * a.zstride + ci * kChunkCols + lane * 4, v);
         }
       }
-      it0 = wave + kLinWaves * kLinPre;
+      it0 = wave + kLinWaves * NPRE;
     }
     for (int it = it0; it < a.batch * nch; it += kLinWaves) {
       const int b = it / nch, ci = it - b * nch;
@@ -207,11 +212,11 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre& f, b
       const int c0 = ci * kChunkCols + lane * 4;
       const int k = (ci - wave) / kLinWaves;  // prefetched item of row 0
       float v[4];
-      if (pre && b == 0 && k < kLinPre) {
-        // (k < kLinPre is uniform: select the registers without indexing)
+      if (pre && b == 0 && k < NPRE) {
+        // (k < NPRE is uniform: select the registers without indexing)
         float t[4];
 #pragma unroll
-        for (int kk = 0; kk < kLinPre; ++kk) {
+        for (int kk = 0; kk < NPRE; ++kk) {
           if (kk == k) {
             lin_pre_product(a, f, kk, ci * kChunkCols, t);
 #pragma unroll
@@ -300,9 +305,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   // B operand halves of this lane inside a unit's staged z (rows past the
   // batch read row 0: their MFMA columns are never written out).
   const int bbz = bb < a.batch ? bb : 0;
-  int zoff[NZ];
-#pragma unroll
-  for (int l = 0; l < NZ; ++l) zoff[l] = bbz * a.zstride + q * kSegCols + mfma_col(l * SLOTS + slot);
+  const int zrow = bbz * a.zstride + q * kSegCols;
   const int lt = wave / a.s;        // local tile of this wave
   const int j = wave - lt * a.s;    // K chunk of this wave
   const int u0 = j * a.c;
@@ -328,9 +331,9 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     // The first group's activations load before its weights (they gate the
     // rotation, which every decode waits for).
     const bool pre = ROT && p != staged && g == (int)blockIdx.x;
-    XPre xf;
+    XPre<lin_pre(KB)> xf;
     if constexpr (ROT) {
-      if (pre) xf = lin_prefetch_x(a, P, wave, lane);
+      if (pre) xf = lin_prefetch_x<lin_pre(KB)>(a, P, wave, lane);
     }
 
     // Every weight load of this wave, then the halo word (path word 1 of
@@ -348,15 +351,13 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     const uint32_t x1_prev = __builtin_amdgcn_raw_buffer_load_b32(
         prs, (active && u0 > 0) ? pv + 4u : kOutOfRange, (uint32_t)(u0 > 0 ? u0 - 1 : 0) * unit_p, 0);
     const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(P.scales, (uint32_t)P.n * 2u);
-    uint32_t sc[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      sc[i] = __builtin_amdgcn_raw_buffer_load_b16(srs, (uint32_t)(tt * kTileRows + 4 * q + i) * 2u, 0, 0);
+    // rows 4q..4q+3 in one 8-byte load (words past n read as zero)
+    const u32x2_t sc = __builtin_amdgcn_raw_buffer_load_b64(srs, (uint32_t)(tt * kTileRows + 4 * q) * 2u, 0, 0);
 
     if (g == (int)blockIdx.x) build_pair_table_lanes<KB>(table, cb_lane, tid, kLinThreads);
     if (p != staged) {
       if (staged >= 0) __syncthreads();  // the previous group's reads of z and scr are done
-      lin_stage_z<ROT>(a, P, xf, pre, zl, scr, tid, wave, lane);
+      lin_stage_z<ROT, lin_pre(KB)>(a, P, xf, pre, zl, scr, tid, wave, lane);
       staged = p;
     }
     __syncthreads();
@@ -371,7 +372,8 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
         if (u < nu) {
           const int cbase = (u0 + u) * kChunkCols;
 #pragma unroll
-          for (int l = 0; l < NZ; ++l) R[u].Z[l] = *reinterpret_cast<const u32x4_t*>(zl + zoff[l] + cbase);
+          for (int l = 0; l < NZ; ++l)
+            R[u].Z[l] = *reinterpret_cast<const u32x4_t*>(zl + zrow + mfma_col(l * SLOTS + slot) + cbase);
           const uint32_t provide = (q == 3) ? prev : R[u].X[1];
           slot_unit<KB, NS, SB, MW, NZ>(R[u], provide, lane, laneoff, table, acc);
           prev = R[u].X[1];
@@ -405,7 +407,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
         for (int i = 0; i < 4; ++i) {
           const int row = row0 + i;
           if (row >= P.n) continue;
-          uint16_t out = f2h(v[i] * h2f((uint16_t)sc[i]));
+          uint16_t out = f2h(v[i] * h2f((uint16_t)(sc[i >> 1] >> (16 * (i & 1)))));
           if (P.bias) out = f2h(h2f(out) + h2f(gld(P.bias + row)));
           gst(P.y + (size_t)bb * P.ldy + row, out);
         }
@@ -454,7 +456,7 @@ void launch_linear_sb(const LinArgs& a, int grid, size_t dyn, bool rot, hipStrea
 int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
                         int bits, int n_states, hipStream_t s) {
   if (batch < 1 || batch > 8 || n_lin < 1 || n_lin > kLinMaxParts) return kLinearNotHandled;
-  if (bits != 2 && bits != 3) return kLinearNotHandled;
+  if (bits < 2 || bits > 4) return kLinearNotHandled;
   const bool rot = ls[0].rot_scale != nullptr;
   const int64_t d = ls[0].d, hb = rot ? ls[0].block : 1;
   for (int i = 1; i < n_lin; ++i)
@@ -469,7 +471,7 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   // Staging issues the activations of two items per wave ahead of the
   // weights; each further item costs a dependent round trip, so larger
   // inputs (batch * 256-column chunks) keep the split-K kernel.
-  if (batch * G4 > (int64_t)kLinWaves * (kLinPre + 1) || batch > 4) return kLinearNotHandled;
+  if (batch * G4 > (int64_t)kLinWaves * (lin_pre(bits) + 1) || batch > 4) return kLinearNotHandled;
 
   // LDS: 64 KiB table (static) + z rows + max(partial sums, one fp32 row).
   const int64_t zstride = G4 * kChunkCols + 8;
@@ -543,6 +545,10 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
     case 308: launch_linear_sb<3, 8>(a, grid, dyn, rot, s); break;
     case 316: launch_linear_sb<3, 16>(a, grid, dyn, rot, s); break;
     case 364: launch_linear_sb<3, 64>(a, grid, dyn, rot, s); break;
+    case 404: launch_linear_sb<4, 4>(a, grid, dyn, rot, s); break;
+    case 408: launch_linear_sb<4, 8>(a, grid, dyn, rot, s); break;
+    case 416: launch_linear_sb<4, 16>(a, grid, dyn, rot, s); break;
+    case 464: launch_linear_sb<4, 64>(a, grid, dyn, rot, s); break;
     default: return TP_ERR_UNSUPPORTED_STATES;
   }
   return launch_status();

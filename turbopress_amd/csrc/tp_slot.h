@@ -26,6 +26,21 @@ template <> struct MemberBuf<4> {
     return __builtin_amdgcn_raw_buffer_load_b128(r, v, s, 0);
   }
 };
+// k=4: six words (the k=3 words, then one high-member word per path word)
+struct MemberWords6 {
+  u32x4_t lo;
+  u32x2_t hi;
+  __device__ __forceinline__ uint32_t operator[](int i) const { return i < 4 ? lo[i] : hi[i - 4]; }
+};
+template <> struct MemberBuf<6> {
+  typedef MemberWords6 type;
+  static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
+    MemberWords6 m;
+    m.lo = __builtin_amdgcn_raw_buffer_load_b128(r, v, s, 0);
+    m.hi = __builtin_amdgcn_raw_buffer_load_b64(r, v + 16u, s, 0);
+    return m;
+  }
+};
 
 // Loads of one unit of one lane.
 template <int MW, int NZ>
@@ -51,11 +66,7 @@ __device__ __forceinline__ void slot_unit(const UnitRegs<MW, NZ>& g, const uint3
   constexpr int SLOTS = 16 / SB;
   const uint32_t halo = (uint32_t)__shfl((int)provide, (lane + 48) & 63, 64);
   MemberWords<KB> m[2];
-  if constexpr (KB == 3) {
-    m[0].a = g.M[0]; m[0].b = g.M[1]; m[1].a = g.M[2]; m[1].b = g.M[3];
-  } else {
-    m[0].w = g.M[0]; m[1].w = g.M[1];
-  }
+  split_members<KB>(g.M, m);
 #pragma unroll
   for (int xi = 0; xi < 2; ++xi) {
     const int x = 1 - xi;

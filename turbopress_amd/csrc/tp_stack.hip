@@ -893,7 +893,7 @@ inline int stack_sizes(const tp_stack_linear* linears, int n_linears, int bits, 
 using namespace tp;
 
 extern "C" int64_t tp_stack_plan_bytes(const tp_stack_linear* linears, int n_linears, int bits, int64_t batch) {
-  if (bits != 2 && bits != 3) return 0;
+  if (bits < 2 || bits > 4) return 0;
   StackSizes z;
   if (stack_sizes(linears, n_linears, bits, batch, &z) != TP_OK) return 0;
   return (int64_t)stack_layout(n_linears, z.n_phases, (int)z.total_blocks, (int)z.n_rot, z.zbuf_bytes).total;
@@ -902,7 +902,7 @@ extern "C" int64_t tp_stack_plan_bytes(const tp_stack_linear* linears, int n_lin
 extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears, int bits,
                                   int64_t batch, void* plan, int64_t plan_bytes) {
   if (!linears || !plan) return TP_ERR_NULL_POINTER;
-  if (bits != 2 && bits != 3) return TP_ERR_UNSUPPORTED_BITS;
+  if (bits < 2 || bits > 4) return TP_ERR_UNSUPPORTED_BITS;
   StackSizes z;
   int st = stack_sizes(linears, n_linears, bits, batch, &z);
   if (st) return st;
@@ -1048,6 +1048,10 @@ extern "C" int tp_stack_gemv(void* plan, int64_t batch, const uint16_t* codebook
     case 308: return launch_gemv<3, 8>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
     case 316: return launch_gemv<3, 16>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
     case 364: return launch_gemv<3, 64>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    case 404: return launch_gemv<4, 4>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    case 408: return launch_gemv<4, 8>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    case 416: return launch_gemv<4, 16>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
+    case 464: return launch_gemv<4, 64>(p, total_blocks, batch, codebook, ordered, spin_limit, s);
     default: return TP_ERR_UNSUPPORTED_STATES;
   }
 }
@@ -1056,10 +1060,8 @@ extern "C" int tp_stack_run(void* plan, int64_t batch, const uint16_t* codebook,
                             int n_states, int ordered, int64_t total_blocks, void* stream) {
   if (!plan || !codebook) return TP_ERR_NULL_POINTER;
   if (total_blocks < 1 || total_blocks > INT32_MAX) return TP_ERR_BAD_DIMS;
-  if (bits * 100 + n_states != 204 && bits * 100 + n_states != 208 && bits * 100 + n_states != 216 &&
-      bits * 100 + n_states != 264 && bits * 100 + n_states != 304 && bits * 100 + n_states != 308 &&
-      bits * 100 + n_states != 316 && bits * 100 + n_states != 364)
-    return TP_ERR_UNSUPPORTED_STATES;
+  if (bits < 2 || bits > 4) return TP_ERR_UNSUPPORTED_BITS;
+  if (n_states != 4 && n_states != 8 && n_states != 16 && n_states != 64) return TP_ERR_UNSUPPORTED_STATES;
   const int st = tp_stack_rotate(plan, batch, stream);
   if (st) return st;
   return tp_stack_gemv(plan, batch, codebook, bits, n_states, ordered, total_blocks, stream);

@@ -14,8 +14,9 @@
 //             then the two nibbles of every byte swapped;
 //        k=2: W[x], bits 4p..4p+1 = members of columns 64g + 16x + 2p, +1 and
 //             bits 4p+2..4p+3 = members of columns 64g + 32 + 16x + 2p, +1;
-//        k=4: the k=3 words of the low two member bits, then the k=2 words of
-//             the high member bit (MW = 6).
+//        k=4: the k=3 words of the low two member bits, then one word per
+//             path word x of the high member bits, laid out for the
+//             decoder's lane-offset bytes (see high_member_word) (MW = 6).
 //
 // Decode (per lane, 32 weights per path word; reference contract
 // turbopress/runtime.py:122-139): the subset bits are parities of the path
@@ -236,11 +237,7 @@ tiled_decode_kernel(const uint32_t* __restrict__ path, const uint32_t* __restric
   uint32_t Mw[MW];
   for (int i = 0; i < MW; ++i) Mw[i] = mt[(g * kTileRows + r) * MW + i];
   MemberWords<KB> mm[2];
-  if constexpr (KB == 3) {
-    mm[0].a = Mw[0]; mm[0].b = Mw[1]; mm[1].a = Mw[2]; mm[1].b = Mw[3];
-  } else {
-    mm[0].w = Mw[0]; mm[1].w = Mw[1];
-  }
+  split_members<KB>(Mw, mm);
   const int row = t * kTileRows + r;
   const float sc = row < n ? h2f(scales[row]) : 0.f;
   for (int x = 0; x < 2; ++x) {
@@ -273,6 +270,21 @@ __device__ __forceinline__ uint32_t interleave16(uint32_t a, uint32_t b) {
 __device__ __forceinline__ uint32_t pair_interleave16(uint32_t a, uint32_t b) {
   uint32_t o = 0;
   for (int p = 0; p < 8; ++p) o |= (((a >> (2 * p)) & 3u) << (4 * p)) | (((b >> (2 * p)) & 3u) << (4 * p + 2));
+  return o;
+}
+
+// k=4 high member bits of path word x (first-half column group f, second
+// half s; bit j = column j of the group), placed where the decoder moves
+// them into bits 6..7 of each lane-offset byte: byte k holds columns 4k, 4k+1
+// of f at bits 6, 7, columns 4k+2, 4k+3 of f at bits 4, 5, columns 4k, 4k+1
+// of s at bits 2, 3 and columns 4k+2, 4k+3 of s at bits 0, 1.
+__device__ __forceinline__ uint32_t high_member_word(uint32_t f, uint32_t s) {
+  uint32_t o = 0;
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t fb = (f >> (4 * k)) & 15u, sb = (s >> (4 * k)) & 15u;
+    o |= ((fb & 3u) << (8 * k + 6)) | (((fb >> 2) & 3u) << (8 * k + 4)) | ((sb & 3u) << (8 * k + 2)) |
+         (((sb >> 2) & 3u) << (8 * k));
+  }
   return o;
 }
 
@@ -327,8 +339,8 @@ __global__ void retile_kernel(const uint8_t* __restrict__ path, int64_t ps,
     mo[0] = pair_interleave16(m1[0], m1[2]);
     mo[1] = pair_interleave16(m1[1], m1[3]);
   } else if (bits == 4) {
-    mo[4] = pair_interleave16(m1[0], m1[2]);
-    mo[5] = pair_interleave16(m1[1], m1[3]);
+    mo[4] = high_member_word(m1[0], m1[2]);
+    mo[5] = high_member_word(m1[1], m1[3]);
   }
 }
 
@@ -383,7 +395,6 @@ extern "C" int tp_decode_tiled(const uint8_t* path_tiled, const uint8_t* member_
   Geom g;
   int st = tiled_geom(n, d, bits, &g);
   if (st) return st;
-  if (bits == 4) return TP_ERR_UNSUPPORTED_BITS;
   if (!path_tiled || !member_tiled || !scales || !codebook || !w_out) return TP_ERR_NULL_POINTER;
   if (out_stride < d) return TP_ERR_BAD_DIMS;
   const int64_t units = g.T * g.G4;
@@ -403,6 +414,10 @@ extern "C" int tp_decode_tiled(const uint8_t* path_tiled, const uint8_t* member_
     case 308: TP_DEC(3, 8); break;
     case 316: TP_DEC(3, 16); break;
     case 364: TP_DEC(3, 64); break;
+    case 404: TP_DEC(4, 4); break;
+    case 408: TP_DEC(4, 8); break;
+    case 416: TP_DEC(4, 16); break;
+    case 464: TP_DEC(4, 64); break;
     default: return TP_ERR_UNSUPPORTED_STATES;
   }
 #undef TP_DEC
@@ -435,7 +450,7 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
                      int bits, int n_states, void* stream) {
   if (n_lin < 1 || n_lin > kMaxInlineLinears) return TP_ERR_BAD_DIMS;
   if (!codebook) return TP_ERR_NULL_POINTER;
-  if (bits != 2 && bits != 3) return TP_ERR_UNSUPPORTED_BITS;
+  if (bits < 2 || bits > 4) return TP_ERR_UNSUPPORTED_BITS;
   if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
   const int nbt = batch <= 16 ? 1 : 2;
   const bool rot = ls[0].rot_scale != nullptr;
@@ -526,6 +541,10 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
     case 308: launch_gemv_kb<3, 8>(a, grid, nbt, rot, s); break;
     case 316: launch_gemv_kb<3, 16>(a, grid, nbt, rot, s); break;
     case 364: launch_gemv_kb<3, 64>(a, grid, nbt, rot, s); break;
+    case 404: launch_gemv_kb<4, 4>(a, grid, nbt, rot, s); break;
+    case 408: launch_gemv_kb<4, 8>(a, grid, nbt, rot, s); break;
+    case 416: launch_gemv_kb<4, 16>(a, grid, nbt, rot, s); break;
+    case 464: launch_gemv_kb<4, 64>(a, grid, nbt, rot, s); break;
     default: return TP_ERR_UNSUPPORTED_STATES;
   }
   return launch_status();

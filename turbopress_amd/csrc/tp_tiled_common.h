@@ -107,12 +107,21 @@ __device__ __forceinline__ uint32_t table_addr(uint32_t idx, uint32_t laneoff, i
 // the returned word.
 template <int KB>
 __device__ __forceinline__ uint32_t lane_offsets(int lane) {
-  if constexpr (KB == 3) {
+  if constexpr (KB == 4) {
+    // 16 copies of 4 bytes per 64-byte row, the copy offset in every byte
+    // (the high member bits of each pair are or-ed into bits 6..7)
+    return ((uint32_t)(lane & 15) << 2) * 0x01010101u;
+  } else if constexpr (KB == 3) {
     const uint32_t c = (uint32_t)(lane & 31) << 2;
     return c | ((128u + c) << 8);
   } else {
     return (uint32_t)lane << 2;
   }
+}
+
+// k=4: LDS byte address (idx byte b) * 256 + (byte b of the lane word).
+__device__ __forceinline__ uint32_t table_addr4(uint32_t idx, uint32_t lanew, int b) {
+  return __builtin_amdgcn_perm(idx, lanew, 0x0C0C0000u | ((4u + b) << 8) | (uint32_t)b);
 }
 
 __device__ __forceinline__ uint32_t lds_word(const uint32_t* table, uint32_t byte_addr) {
@@ -123,6 +132,20 @@ __device__ __forceinline__ uint32_t lds_word(const uint32_t* table, uint32_t byt
 template <int KB> struct MemberWords;
 template <> struct MemberWords<2> { uint32_t w; };
 template <> struct MemberWords<3> { uint32_t a, b; };
+template <> struct MemberWords<4> { uint32_t a, b, q; };
+
+// Member words of interleaved path words x = 0, 1 from the member_words(KB)
+// words of one segment.
+template <int KB, typename W>
+__device__ __forceinline__ void split_members(const W& w, MemberWords<KB> m[2]) {
+  if constexpr (KB == 4) {
+    m[0].a = w[0]; m[0].b = w[1]; m[1].a = w[2]; m[1].b = w[3]; m[0].q = w[4]; m[1].q = w[5];
+  } else if constexpr (KB == 3) {
+    m[0].a = w[0]; m[0].b = w[1]; m[1].a = w[2]; m[1].b = w[3];
+  } else {
+    m[0].w = w[0]; m[1].w = w[1];
+  }
+}
 
 // Decode 32 weights (16 of each half) of one lane into four MFMA A operands:
 // A[0]/A[1] = first-half columns 0-7 / 8-15, A[2]/A[3] = second half.
@@ -131,33 +154,59 @@ __device__ __forceinline__ void decode_word(uint32_t cur, uint32_t prev, const M
                                             const uint32_t* table, uint32_t laneoff, u32x4_t A[4]) {
   uint32_t SA, SB;
   subset_words<NS>(cur, prev, SA, SB);
-  uint32_t iae, iao, ibe, ibo;
-  constexpr int FO = KB == 3 ? 1 : 0;  // table format of the odd-pair index words
-  if constexpr (KB == 3) {
-    // Member words are stored nibble-swapped within each byte, so one bit
-    // select pairs every subset nibble with its member nibble: even pairs as
-    // [subset | member << 4] (format 0), odd pairs as [member | subset << 4]
-    // (format 1).
-    iae = (SA & 0x0F0F0F0Fu) | (M.a & 0xF0F0F0F0u);
-    iao = (SA & 0xF0F0F0F0u) | (M.a & 0x0F0F0F0Fu);
-    ibe = (SB & 0x0F0F0F0Fu) | (M.b & 0xF0F0F0F0u);
-    ibo = (SB & 0xF0F0F0F0u) | (M.b & 0x0F0F0F0Fu);
-  } else {
-    iae = (SA & 0x0F0F0F0Fu) | ((M.w << 4) & 0xF0F0F0F0u);
-    iao = ((SA >> 4) & 0x0F0F0F0Fu) | (M.w & 0xF0F0F0F0u);
-    ibe = (SB & 0x0F0F0F0Fu) | ((M.w << 2) & 0xF0F0F0F0u);
-    ibo = ((SB >> 4) & 0x0F0F0F0Fu) | ((M.w >> 2) & 0xF0F0F0F0u);
-  }
+  if constexpr (KB == 4) {
+    // One table format: index byte [S0a S1a S0b S1b | M0a M1a M0b M1b] of the
+    // low member bits (odd pairs shifted into place), the pair's two high
+    // member bits into bits 6..7 of the lane-offset byte (row within the
+    // index byte's 256-byte group).
+    const uint32_t iae = (SA & 0x0F0F0F0Fu) | (M.a & 0xF0F0F0F0u);
+    const uint32_t iao = ((SA >> 4) & 0x0F0F0F0Fu) | ((M.a << 4) & 0xF0F0F0F0u);
+    const uint32_t ibe = (SB & 0x0F0F0F0Fu) | (M.b & 0xF0F0F0F0u);
+    const uint32_t ibo = ((SB >> 4) & 0x0F0F0F0Fu) | ((M.b << 4) & 0xF0F0F0F0u);
+    const uint32_t lae = (M.q & 0xC0C0C0C0u) | laneoff;
+    const uint32_t lao = ((M.q << 2) & 0xC0C0C0C0u) | laneoff;
+    const uint32_t lbe = ((M.q << 4) & 0xC0C0C0C0u) | laneoff;
+    const uint32_t lbo = ((M.q << 6) & 0xC0C0C0C0u) | laneoff;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    A[0][2 * h] = lds_word(table, table_addr<0>(iae, laneoff, h));
-    A[0][2 * h + 1] = lds_word(table, table_addr<FO>(iao, laneoff, h));
-    A[1][2 * h] = lds_word(table, table_addr<0>(iae, laneoff, 2 + h));
-    A[1][2 * h + 1] = lds_word(table, table_addr<FO>(iao, laneoff, 2 + h));
-    A[2][2 * h] = lds_word(table, table_addr<0>(ibe, laneoff, h));
-    A[2][2 * h + 1] = lds_word(table, table_addr<FO>(ibo, laneoff, h));
-    A[3][2 * h] = lds_word(table, table_addr<0>(ibe, laneoff, 2 + h));
-    A[3][2 * h + 1] = lds_word(table, table_addr<FO>(ibo, laneoff, 2 + h));
+    for (int h = 0; h < 2; ++h) {
+      A[0][2 * h] = lds_word(table, table_addr4(iae, lae, h));
+      A[0][2 * h + 1] = lds_word(table, table_addr4(iao, lao, h));
+      A[1][2 * h] = lds_word(table, table_addr4(iae, lae, 2 + h));
+      A[1][2 * h + 1] = lds_word(table, table_addr4(iao, lao, 2 + h));
+      A[2][2 * h] = lds_word(table, table_addr4(ibe, lbe, h));
+      A[2][2 * h + 1] = lds_word(table, table_addr4(ibo, lbo, h));
+      A[3][2 * h] = lds_word(table, table_addr4(ibe, lbe, 2 + h));
+      A[3][2 * h + 1] = lds_word(table, table_addr4(ibo, lbo, 2 + h));
+    }
+  } else {
+    uint32_t iae, iao, ibe, ibo;
+    constexpr int FO = KB == 3 ? 1 : 0;  // table format of the odd-pair index words
+    if constexpr (KB == 3) {
+      // Member words are stored nibble-swapped within each byte, so one bit
+      // select pairs every subset nibble with its member nibble: even pairs as
+      // [subset | member << 4] (format 0), odd pairs as [member | subset << 4]
+      // (format 1).
+      iae = (SA & 0x0F0F0F0Fu) | (M.a & 0xF0F0F0F0u);
+      iao = (SA & 0xF0F0F0F0u) | (M.a & 0x0F0F0F0Fu);
+      ibe = (SB & 0x0F0F0F0Fu) | (M.b & 0xF0F0F0F0u);
+      ibo = (SB & 0xF0F0F0F0u) | (M.b & 0x0F0F0F0Fu);
+    } else {
+      iae = (SA & 0x0F0F0F0Fu) | ((M.w << 4) & 0xF0F0F0F0u);
+      iao = ((SA >> 4) & 0x0F0F0F0Fu) | (M.w & 0xF0F0F0F0u);
+      ibe = (SB & 0x0F0F0F0Fu) | ((M.w << 2) & 0xF0F0F0F0u);
+      ibo = ((SB >> 4) & 0x0F0F0F0Fu) | ((M.w >> 2) & 0xF0F0F0F0u);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      A[0][2 * h] = lds_word(table, table_addr<0>(iae, laneoff, h));
+      A[0][2 * h + 1] = lds_word(table, table_addr<FO>(iao, laneoff, h));
+      A[1][2 * h] = lds_word(table, table_addr<0>(iae, laneoff, 2 + h));
+      A[1][2 * h + 1] = lds_word(table, table_addr<FO>(iao, laneoff, 2 + h));
+      A[2][2 * h] = lds_word(table, table_addr<0>(ibe, laneoff, h));
+      A[2][2 * h + 1] = lds_word(table, table_addr<FO>(ibo, laneoff, h));
+      A[3][2 * h] = lds_word(table, table_addr<0>(ibe, laneoff, 2 + h));
+      A[3][2 * h + 1] = lds_word(table, table_addr<FO>(ibo, laneoff, 2 + h));
+    }
   }
 }
 
@@ -184,8 +233,28 @@ __device__ __forceinline__ void pair_fields(uint32_t v, int fmt, uint32_t& sa, u
   }
 }
 
+// k=4 table: 1024 rows of 64 bytes (16 lane copies); row 4v + m2a + 2 m2b
+// holds (cb[level_a] | cb[level_b] << 16) for index byte v in format 0 and
+// high member bits m2a, m2b (level = member * 4 + subset, member = low 2
+// bits + 4 * high bit).  Run i (16 bytes) belongs to row i / 4.
+__device__ __forceinline__ void pair_levels4(int i, uint32_t& la, uint32_t& lb) {
+  const uint32_t row = (uint32_t)i >> 2, v = row >> 2;
+  la = ((((v >> 4) & 3u) + 4u * (row & 1u)) << 2) | (v & 3u);
+  lb = ((((v >> 6) & 3u) + 4u * ((row >> 1) & 1u)) << 2) | ((v >> 2) & 3u);
+}
+
 template <int KB>
 __device__ void build_pair_table(uint32_t* table, const uint16_t* cb, int tid, int nthreads) {
+  if constexpr (KB == 4) {
+    for (int i = tid; i < kTableWords / 4; i += nthreads) {
+      uint32_t la, lb;
+      pair_levels4(i, la, lb);
+      const uint32_t e = (uint32_t)cb[la] | ((uint32_t)cb[lb] << 16);
+      u32x4_t run = {e, e, e, e};
+      *reinterpret_cast<u32x4_t*>(table + 4 * i) = run;
+    }
+    return;
+  }
   // Each thread writes 16-byte runs (4 lane copies) of one entry: 16 runs
   // per row, runs 8..15 are format 1 for k=3.
   for (int i = tid; i < kTableWords / 4; i += nthreads) {
@@ -202,6 +271,18 @@ __device__ void build_pair_table(uint32_t* table, const uint16_t* cb, int tid, i
 // no memory reads, entries gathered with lane shuffles.
 template <int KB>
 __device__ void build_pair_table_lanes(uint32_t* table, uint32_t cb_lane, int tid, int nthreads) {
+  if constexpr (KB == 4) {
+    for (int i = tid; i < kTableWords / 4; i += nthreads) {
+      uint32_t la, lb;
+      pair_levels4(i, la, lb);
+      const uint32_t lo = (uint32_t)__shfl((int)cb_lane, (int)la, 64);
+      const uint32_t hi = (uint32_t)__shfl((int)cb_lane, (int)lb, 64);
+      const uint32_t e = (lo & 0xFFFFu) | (hi << 16);
+      u32x4_t run = {e, e, e, e};
+      *reinterpret_cast<u32x4_t*>(table + 4 * i) = run;
+    }
+    return;
+  }
   for (int i = tid; i < kTableWords / 4; i += nthreads) {
     const uint32_t v = (uint32_t)(i >> 4);
     uint32_t sa, sb, ma, mb;
@@ -505,11 +586,7 @@ __device__ __forceinline__ void process_unit(const uint2 X, const uint32_t* Mw, 
   const uint32_t halo = (uint32_t)__shfl((int)provide, (lane + 48) & 63, 64);
   const uint32_t P = ((halo >> 1) & 0x55555555u) | ((X.y << 1) & 0xAAAAAAAAu);
   MemberWords<KB> m[2];
-  if constexpr (KB == 3) {
-    m[0].a = Mw[0]; m[0].b = Mw[1]; m[1].a = Mw[2]; m[1].b = Mw[3];
-  } else {
-    m[0].w = Mw[0]; m[1].w = Mw[1];
-  }
+  split_members<KB>(Mw, m);
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
     // B operands of this interleaved word's 4 MFMAs (batch column r).

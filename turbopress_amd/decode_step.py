@@ -44,7 +44,7 @@ class LinearStack:
         l0 = lins[0]
         for lin in lins:
             if lin.tiled_packed is None:
-                raise ValueError("stack linears need mode='hip' with bits in (2, 3)")
+                raise ValueError("stack linears need mode='hip' with bits in (2, 3, 4)")
             if (lin.bits, lin.n_states) != (l0.bits, l0.n_states) or lin.codebook_key != l0.codebook_key:
                 raise ValueError("stack linears must share bits, n_states and codebook")
         self.linears = lins

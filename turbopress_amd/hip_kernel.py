@@ -19,7 +19,7 @@ __all__ = ["HAS_HIP", "fwht_scale", "packed_gemv", "decode_rows", "window_decode
            "subset_lut", "current_stream_ptr", "tiled_layout", "retile", "TILED_BITS"]
 
 # bits per weight served by the device-layout MFMA kernels
-TILED_BITS = (2, 3)
+TILED_BITS = (2, 3, 4)
 
 
 def _has_hip() -> bool:
