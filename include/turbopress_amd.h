@@ -138,8 +138,7 @@ int tp_tcq_gemv(const uint16_t* z, int64_t batch,
                 uint16_t* y, void* stream);
 
 /* ---------------------------------------------------------------------------
- * Bandwidth path: device layout + MFMA decode-GEMV (bits 2 and 3; re-tiling
- * also accepts bits 4)
+ * Bandwidth path: device layout + MFMA decode-GEMV (bits 2, 3 and 4)
  * ------------------------------------------------------------------------- */
 
 /* Geometry of the device layout of an n x d linear at `bits`: 16-row tiles,
@@ -170,7 +169,7 @@ int64_t tp_gemv_workspace_bytes(int64_t n, int64_t batch);
 /* y[b, r] = fp16(scale[r] * sum_c codebook[level[r, c]] * z[b, c]) (+ bias),
  * reading the device layout.  z: fp16 [batch, ldz] rotated activations, zero
  * in columns [d, ldz), ldz >= z_cols and a multiple of 8, 16-byte aligned;
- * y: fp16 [batch, ldy]; batch in [1, 32]; bits in {2, 3}; n_states in
+ * y: fp16 [batch, ldy]; batch in [1, 32]; bits in {2, 3, 4}; n_states in
  * {4, 8, 16, 64}.  Calls that overlap on one workspace race.
  * Replaces turbopress/triton_kernel.py:132-157 (packed_gemv). */
 int tp_tcq_gemv_tiled(const uint16_t* z, int64_t ldz, int64_t batch,
@@ -240,7 +239,8 @@ int64_t tp_stack_plan_bytes(const tp_stack_linear* linears, int n_linears, int b
 
 /* Validate the linears and write the plan (descriptors, block prefix sums,
  * phase tables, zeroed counters, batch in [1, 32]) into `plan` (device
- * memory, 256-byte aligned) with a blocking copy.  Setup call, not capturable.  bits in {2, 3}.
+ * memory, 256-byte aligned) with a blocking copy.  Setup call, not capturable.
+ * bits in {2, 3, 4}.
  * No reference counterpart: the reference has no step-level executor; this
  * serves the decode step of scripts/graph_decode_bench.py:70-118. */
 int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears, int bits,
@@ -279,7 +279,7 @@ int tp_stack_error(const void* plan, int* error_out);
 
 /* Decode the device layout through the same decode path the tiled GEMV uses:
  * w[r, c] = fp16(f32(codebook[level]) * f32(scales[r])), fp16 [n, out_stride].
- * bits in {2, 3}.  The bit-exact check of the bandwidth path.
+ * bits in {2, 3, 4}.  The bit-exact check of the bandwidth path.
  * Replaces turbopress/runtime.py:291-301 (decode_rows) for this layout. */
 int tp_decode_tiled(const uint8_t* path_tiled, const uint8_t* member_tiled,
                     const uint16_t* scales, const uint16_t* codebook,
