@@ -29,8 +29,9 @@
 //      own accumulator); the valid column of each accumulator is summed
 //      across slots once per block.  The LDS then only serves the codebook
 //      pair table, whose lookups bound the kernel's issue rate.
-// Batch 9..32 runs tcq_stack_lds_kernel: the workgroup rotates each
-// 512-column chunk of x into LDS and all waves read it as B operands.
+// Batch 9..32 runs tcq_stack_wide_kernel after the same rotation launch:
+// 16-wave workgroups stage the rotated activations through LDS in 512-column
+// chunks (double buffered) and every wave reads them as MFMA B operands.
 #include "tp_tiled_common.h"
 #include "tp_slot.h"
 
@@ -72,6 +73,8 @@ struct StackInfo {
   int32_t n_rot;          // rotation tiles (batch * 4096-column tiles per linear) when the plan has a z buffer
   int32_t min_g4;         // shortest K of the plan in 256-column units
   int64_t zbuf_bytes;
+  int32_t total_wide;     // wide blocks (16 tiles x full K) of the batch 9..32 kernel
+  int32_t reserved;
 };
 
 // One rotation tile (4096 columns of one batch row of one linear's input),
@@ -92,7 +95,7 @@ struct RotItem {
 static_assert(sizeof(RotItem) == 64, "one 16-dword scalar load per rotation tile");
 
 struct StackLayout {
-  size_t rot_items, lin, prefix, lphase, pblocks, sched_o, sched_u, pdone, zbuf, total;
+  size_t rot_items, lin, prefix, lphase, pblocks, sched_o, sched_u, sched_wo, sched_wu, pdone, zbuf, total;
 };
 
 constexpr size_t kStackRO = sizeof(StackCounters);
@@ -126,6 +129,10 @@ __host__ __device__ inline StackLayout stack_layout(int n_lin, int n_phases, int
   o += sizeof(int32_t) * (size_t)total_blocks;
   p.sched_u = o;
   o += sizeof(int32_t) * (size_t)total_blocks;
+  p.sched_wo = o;  // wide schedules: at most one entry per 8-tile block
+  o += sizeof(int32_t) * (size_t)total_blocks;
+  p.sched_wu = o;
+  o += sizeof(int32_t) * (size_t)total_blocks;
   o = (o + 63) & ~(size_t)63;
   p.pdone = o;
   o += sizeof(uint32_t) * (size_t)n_phases;
@@ -144,6 +151,8 @@ struct StackRO {  // views into the read-only part
   const int32_t* pblocks;  // [n_phases] blocks per phase
   const int32_t* sched_o;  // [total] (linear << 20) | block, phase order
   const int32_t* sched_u;  // [total] same blocks, longest K first
+  const int32_t* sched_wo; // [total_wide] (linear << 20) | wide block, phase order
+  const int32_t* sched_wu; // [total_wide] same, longest K first
   size_t pdone;            // byte offset of pdone from the plan start
   size_t zbuf;             // byte offset of the z buffer from the plan start
 };
@@ -161,6 +170,8 @@ __device__ inline StackRO stack_ro(const char* __restrict__ ro) {
   v.pblocks = reinterpret_cast<const int32_t*>(ro + (l.pblocks - kStackRO));
   v.sched_o = reinterpret_cast<const int32_t*>(ro + (l.sched_o - kStackRO));
   v.sched_u = reinterpret_cast<const int32_t*>(ro + (l.sched_u - kStackRO));
+  v.sched_wo = reinterpret_cast<const int32_t*>(ro + (l.sched_wo - kStackRO));
+  v.sched_wu = reinterpret_cast<const int32_t*>(ro + (l.sched_wu - kStackRO));
   v.pdone = l.pdone;
   v.zbuf = l.zbuf;
   return v;
@@ -644,8 +655,20 @@ tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
 }
 
 // ---------------------------------------------------------------------------
-// 3. LDS-staged kernel (batch 9..32)
+// 3. wide kernel (batch 9..32)
 // ---------------------------------------------------------------------------
+// One workgroup of 16 waves per CU takes *wide blocks* (16 row tiles x the
+// full K of one linear) by ticket; wave w owns tile w.  The linear's rotated
+// activations (the plan's z buffer, written by the rotation launch) pass
+// through LDS in chunks of 512 columns x up to 32 batch rows, double
+// buffered: while a chunk is decoded and multiplied, the next one is loaded
+// into registers, then stored to the other buffer before the chunk's one
+// barrier.  Per unit a wave decodes 4096 weights once and issues 8 MFMAs per
+// 16-column batch tile against B operands read from LDS.
+constexpr int kWideWaves = 16;
+constexpr int kWideThreads = 64 * kWideWaves;
+constexpr int kWideChunkHalves = 32 * kZCols;  // one staged chunk (32 rows x 512 columns)
+
 // Path/member words of one chunk (kMaxUnitsPerBlock units) of one lane.
 template <int MW>
 struct ChunkRegs {
@@ -671,51 +694,174 @@ __device__ __forceinline__ ChunkRegs<MW> load_chunk(const LinearDesc& L, const u
   return c;
 }
 
+struct ZChunk {
+  u32x4_t v[2];
+};
+
+// Thread tid's two 16-byte pieces of chunk ch: piece i = tid + 1024 k is row
+// i / 64, columns 8 (i % 64) ..; rows past the batch are not loaded.
+__device__ __forceinline__ ZChunk wide_load_z(__amdgpu_buffer_rsrc_t zrs, int zld, int batch, int ch, int tid) {
+  ZChunk c;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = tid + kWideThreads * k;
+    const int row = i >> 6, c8 = (i & 63) * 8;
+    const uint32_t off = row < batch ? (uint32_t)(row * zld + ch * kZCols + c8) * 2u : kOutOfRange;
+    c.v[k] = __builtin_amdgcn_raw_buffer_load_b128(zrs, off, 0, 0);
+  }
+  return c;
+}
+
+__device__ __forceinline__ void wide_store_z(uint16_t* zb, const ZChunk& c, int batch, int tid) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = tid + kWideThreads * k;
+    const int row = i >> 6, c8 = (i & 63) * 8;
+    if (row < batch) *reinterpret_cast<u32x4_t*>(zb + zl_index(row, c8)) = c.v[k];
+  }
+}
+
+// One unit of one wave of the wide kernel: decode 64 weights per lane, then
+// for each of the 8 MFMA positions read the B operands of the NBT batch tiles
+// from the staged chunk (rows past the batch hold stale data: their MFMA
+// columns are never written out).
 template <int KB, int NS, int NBT>
-__global__ void __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(2)))
-tcq_stack_lds_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
-                     const uint16_t* __restrict__ codebook, int ordered, int spin_limit, int zrows) {
+__device__ __forceinline__ void wide_unit(const uint2 X, const uint32_t* Mw, const uint32_t x1_last, const int gu,
+                                          const int lc, const int q, const int r, const int lane,
+                                          const uint32_t laneoff, const uint32_t* table, const uint16_t* zb,
+                                          float4_t* acc) {
+  const uint32_t provide = (q == 3) ? (gu == 0 ? 0u : x1_last) : X.y;
+  const uint32_t halo = (uint32_t)__shfl((int)provide, (lane + 48) & 63, 64);
+  const uint32_t P = ((halo >> 1) & 0x55555555u) | ((X.y << 1) & 0xAAAAAAAAu);
+  MemberWords<KB> m[2];
+  split_members<KB>(Mw, m);
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    u32x4_t A[4];
+    decode_word<KB, NS>(x ? X.y : X.x, x ? X.x : P, m[x], table, laneoff, A);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int off = 16 * x + (j & 2 ? 32 : 0) + (j & 1 ? 8 : 0);
+      const half8_t av = __builtin_bit_cast(half8_t, A[j]);
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        const half8_t b = *reinterpret_cast<const half8_t*>(zb + zl_index(bt * 16 + r, lc + off));
+        acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[bt], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// Wide block wb of linear L: z rows at z + b * zld (fp16, zero past d).
+template <int KB, int NS, int NBT>
+__device__ void wide_block(const LinearDesc& L, int wb, const uint16_t* z, int zld, int batch, uint16_t* zl,
+                           const uint32_t* table, uint32_t laneoff, int tid, int wave, int lane) {
+  constexpr int MW = member_words(KB);
+  const int r = lane & 15, q = lane >> 4;
+  const int t = wb * kWideWaves + wave;
+  const bool active = t < L.T;
+  const int nch = (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock;
+  const uint32_t* pt = L.path + (size_t)(active ? t : 0) * L.G * (kTileRows * 2);
+  const uint32_t* mt = L.member + (size_t)(active ? t : 0) * L.G * (kTileRows * MW);
+  const __amdgpu_buffer_rsrc_t zrs = buffer_rsrc(z, (uint32_t)(batch * zld) * 2u);
+
+  float4_t acc[NBT];
+#pragma unroll
+  for (int bt = 0; bt < NBT; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  uint32_t x1_last = 0;
+  {
+    const ZChunk c0 = wide_load_z(zrs, zld, batch, 0, tid);
+    wide_store_z(zl, c0, batch, tid);
+  }
+  __syncthreads();
+  // Chunk ch: prefetch chunk ch + 1 of z, decode + multiply ch, store the
+  // prefetch into the other buffer, one barrier (the next chunk's buffer is
+  // full and nobody still reads the one it will overwrite).
+  auto body = [&](int ch, const ChunkRegs<MW>& regs) {
+    const bool more = ch + 1 < nch;
+    ZChunk nx;
+    if (more) nx = wide_load_z(zrs, zld, batch, ch + 1, tid);
+    const uint16_t* zb = zl + (ch & 1) * kWideChunkHalves;
+    if (active) {
+      const int gu0 = ch * kMaxUnitsPerBlock;
+      const int ngu = min(kMaxUnitsPerBlock, L.G4 - gu0);
+#pragma unroll
+      for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
+        if (u < ngu) {
+          const int gu = gu0 + u;
+          wide_unit<KB, NS, NBT>(regs.X[u], regs.M[u], x1_last, gu, (4 * gu + q - 4 * gu0) * kSegCols, q, r,
+                                 lane, laneoff, table, zb, acc);
+          x1_last = regs.X[u].y;
+        }
+      }
+    }
+    if (more) wide_store_z(zl + ((ch + 1) & 1) * kWideChunkHalves, nx, batch, tid);
+    __syncthreads();
+  };
+  ChunkRegs<MW> ra = load_chunk<MW>(L, pt, mt, 0, q, r);
+  for (int ch = 0; ch < nch; ch += 2) {
+    const ChunkRegs<MW> rb = load_chunk<MW>(L, pt, mt, ch + 1 < nch ? ch + 1 : ch, q, r);
+    body(ch, ra);
+    if (ch + 1 >= nch) break;
+    ra = load_chunk<MW>(L, pt, mt, ch + 2 < nch ? ch + 2 : ch, q, r);
+    body(ch + 1, rb);
+  }
+
+  // Full-K epilogue: lane holds rows 4q..4q+3 of its tile for batch column r.
+  if (active) {
+    const int row0 = t * kTileRows + 4 * q;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = row0 + i;
+      if (row >= L.n) continue;
+      const float sc = h2f(gld(L.scales + row));
+      const float bs = L.bias ? h2f(gld(L.bias + row)) : 0.f;
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        const int nb = bt * 16 + r;
+        if (nb >= batch) continue;
+        uint16_t out = f2h(acc[bt][i] * sc);
+        if (L.bias) out = f2h(h2f(out) + bs);
+        gst(L.y + (size_t)nb * L.ldy + row, out);
+      }
+    }
+  }
+}
+
+template <int KB, int NS, int NBT>
+__global__ void __launch_bounds__(kWideThreads)
+tcq_stack_wide_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
+                      const uint16_t* __restrict__ codebook, int ordered, int spin_limit) {
   __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
   extern __shared__ __attribute__((aligned(16))) uint16_t zl[];
   __shared__ int s_next;
-  constexpr int MW = member_words(KB);
   // Sizes come from the plan itself, never from the caller.
   const StackRO P = stack_ro(plan_ro);
   const int batch = P.info->batch;
-  const int total = P.info->total_blocks;
+  const int total = P.info->total_wide;
   StackCounters* C = reinterpret_cast<StackCounters*>(plan_rw);
   uint32_t* pdone = reinterpret_cast<uint32_t*>(plan_rw + P.pdone);
-  if (batch > 16 * NBT || batch > zrows) {  // staged z rows would not fit: refuse uniformly
+  if (batch > 16 * NBT || P.info->zbuf_bytes == 0) {  // not a plan for this kernel: refuse uniformly
     if (threadIdx.x == 0 && blockIdx.x == 0) atomicExch(&C->error, 2u);
     return;
   }
-  const int32_t* sched = ordered ? P.sched_o : P.sched_u;
+  const int32_t* sched = ordered ? P.sched_wo : P.sched_wu;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int r = lane & 15;
-  const int q = lane >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t laneoff = lane_offsets<KB>(lane);
   const uint32_t cb_lane = gld(codebook + (lane & ((2 << KB) - 1)));
 
   if (tid == 0) s_next = (int)atomicAdd(&C->ticket, 1u);
-  build_pair_table_lanes<KB>(table, cb_lane, tid, kGroupThreads);
+  build_pair_table_lanes<KB>(table, cb_lane, tid, kWideThreads);
   __syncthreads();
-  // The ticket travels through LDS; make its uniformity explicit so that the
-  // descriptor reads below become scalar loads.
   int blk = __builtin_amdgcn_readfirstlane(s_next);
 
   while (blk < total) {
     const int e = sched[blk];
     const int li = __builtin_amdgcn_readfirstlane(e >> kStackBlockBits);
-    const int lb = e & ((1 << kStackBlockBits) - 1);
+    const int wb = e & ((1 << kStackBlockBits) - 1);
     const LinearDesc L = P.lin[li];  // copied to registers once per block
-    const int t = lb * kWavesPerGroup + wave;
-    const bool active = t < L.T;
-    const int nch = (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock;
-    const uint32_t* pt = L.path + (size_t)(active ? t : 0) * L.G * (kTileRows * 2);
-    const uint32_t* mt = L.member + (size_t)(active ? t : 0) * L.G * (kTileRows * MW);
-
     uint32_t next_ticket = 0;
     if (tid == 0) next_ticket = atomicAdd(&C->ticket, 1u);
     if (ordered) {
@@ -725,60 +871,12 @@ tcq_stack_lds_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_r
         __syncthreads();
       }
     }
-
-    uint32_t x1_last = 0;
-    float4_t acc[NBT];
-#pragma unroll
-    for (int bt = 0; bt < NBT; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
-    auto chunk_body = [&](int ch, const ChunkRegs<MW>& regs) {
-      const int gu0 = ch * kMaxUnitsPerBlock;
-      const int ngu = min(kMaxUnitsPerBlock, L.G4 - gu0);
-      __syncthreads();  // z of the previous chunk is no longer read
-      stage_z<true>(L, gu0, ngu, batch, zl, wave, lane);
-      __syncthreads();
-      if (active) {
-#pragma unroll
-        for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
-          if (u >= ngu) break;
-          const int gu = gu0 + u;
-          process_unit<KB, NS, NBT>(regs.X[u], regs.M[u], x1_last, gu, (4 * gu + q - 4 * gu0) * kSegCols, q, r,
-                                    lane, laneoff, table, zl, batch, acc);
-          x1_last = regs.X[u].y;
-        }
-      }
-    };
-    ChunkRegs<MW> ra = load_chunk<MW>(L, pt, mt, 0, q, r);
-    for (int ch = 0; ch < nch; ch += 2) {
-      const ChunkRegs<MW> rb = load_chunk<MW>(L, pt, mt, ch + 1 < nch ? ch + 1 : ch, q, r);
-      chunk_body(ch, ra);
-      if (ch + 1 >= nch) break;
-      ra = load_chunk<MW>(L, pt, mt, ch + 2 < nch ? ch + 2 : ch, q, r);
-      chunk_body(ch + 1, rb);
-    }
-
-    // Full-K epilogue: lane holds rows 4q..4q+3 of its tile for batch column r.
-    if (active) {
-      const int row0 = t * kTileRows + 4 * q;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = row0 + i;
-        if (row >= L.n) continue;
-        const float sc = h2f(gld(L.scales + row));
-        const float bs = L.bias ? h2f(gld(L.bias + row)) : 0.f;
-#pragma unroll
-        for (int bt = 0; bt < NBT; ++bt) {
-          const int nb = bt * 16 + r;
-          if (nb >= batch) continue;
-          uint16_t out = f2h(acc[bt][i] * sc);
-          if (L.bias) out = f2h(h2f(out) + bs);
-          gst(L.y + (size_t)nb * L.ldy + row, out);
-        }
-      }
-    }
+    wide_block<KB, NS, NBT>(L, wb, L.z, L.G4 * kChunkCols, batch, zl, table, laneoff, tid, wave, lane);
     if (ordered) {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
-      if (tid == 0) atomicAdd(&pdone[P.lphase[li]], 1u);
+      // phase counts are in 8-tile blocks: a wide block covers two (one at the end)
+      if (tid == 0) atomicAdd(&pdone[P.lphase[li]], (uint32_t)min(2, L.blocks - 2 * wb));
     }
     if (tid == 0) s_next = (int)next_ticket;
     __syncthreads();
@@ -794,10 +892,6 @@ tcq_stack_lds_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_r
     }
   }
 }
-
-// z staging rows of the LDS kernel: 16 rows (batch <= 16) keep table + z
-// within 80 KiB (two workgroups per CU); 32 rows need one workgroup per CU.
-inline int stack_z_rows(int64_t batch) { return batch <= 16 ? 16 : 32; }
 
 inline int slot_batch(int64_t batch) { return batch <= 4 ? 4 : 8; }
 
@@ -824,9 +918,8 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
                 int spin_limit, hipStream_t s) {
   const char* ro = plan + kStackRO;
   const int cus = device_cu_count();
-  const int per_cu = batch <= 16 ? 2 : 1;
-  const int grid = (int)(total_blocks < (int64_t)cus * per_cu ? total_blocks : (int64_t)cus * per_cu);
   if (batch <= kSlotMaxBatch) {
+    const int grid = (int)(total_blocks < (int64_t)cus * 2 ? total_blocks : (int64_t)cus * 2);
     const int sb = slot_batch(batch);
     PlanArgs pa = {0, 0, 0, 0};
     PlanReg reg;
@@ -839,20 +932,26 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
       hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 8>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
                          ordered, spin_limit, pa);
   } else {
-    const int zr = stack_z_rows(batch);
-    const size_t zbytes = (size_t)zr * kZCols * 2;
-    if (batch <= 16)
-      hipLaunchKernelGGL((tcq_stack_lds_kernel<KB, NS, 1>), dim3(grid), dim3(kGroupThreads), zbytes, s, ro, plan,
-                         cb, ordered, spin_limit, zr);
-    else
-      hipLaunchKernelGGL((tcq_stack_lds_kernel<KB, NS, 2>), dim3(grid), dim3(kGroupThreads), zbytes, s, ro, plan,
-                         cb, ordered, spin_limit, zr);
+    // one 16-wave workgroup per CU (64 KiB table + two 32 KiB z chunks)
+    const int grid = (int)(total_blocks < (int64_t)cus ? total_blocks : (int64_t)cus);
+    const size_t zbytes = (size_t)2 * kWideChunkHalves * 2;
+    if (batch <= 16) {
+      auto kern = tcq_stack_wide_kernel<KB, NS, 1>;
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)zbytes);
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(kWideThreads), zbytes, s, ro, plan, cb, ordered, spin_limit);
+    } else {
+      auto kern = tcq_stack_wide_kernel<KB, NS, 2>;
+      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)zbytes);
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(kWideThreads), zbytes, s, ro, plan, cb, ordered, spin_limit);
+    }
   }
   return launch_status();
 }
 
 
-// Host-side sizes of a stack (validated); zbuf_bytes and n_rot are 0 for batch > 8.
+// Host-side sizes of a stack (validated).
 struct StackSizes {
   int n_phases;
   int64_t total_blocks, n_rot, zbuf_bytes, min_g4;
@@ -876,10 +975,8 @@ inline int stack_sizes(const tp_stack_linear* linears, int n_linears, int bits, 
     if (blocks >= (1 << kStackBlockBits)) return TP_ERR_BAD_DIMS;
     z.total_blocks += blocks;
     if (g.G4 < z.min_g4) z.min_g4 = g.G4;
-    if (batch <= kSlotMaxBatch) {
-      z.n_rot += batch * rot_tiles((int)g.G4);
-      z.zbuf_bytes += zbuf_linear_bytes(batch, g.G4);
-    }
+    z.n_rot += batch * rot_tiles((int)g.G4);
+    z.zbuf_bytes += zbuf_linear_bytes(batch, g.G4);
   }
   // z buffer offsets are 32-bit and lanes past the batch read at 2^31: keep it below 2 GiB
   if (z.total_blocks > INT32_MAX / 2 || z.n_rot > INT32_MAX || z.zbuf_bytes >= ((int64_t)1 << 31))
@@ -920,6 +1017,8 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
   int32_t* pblocks = reinterpret_cast<int32_t*>(host + lay.pblocks);
   int32_t* sched_o = reinterpret_cast<int32_t*>(host + lay.sched_o);
   int32_t* sched_u = reinterpret_cast<int32_t*>(host + lay.sched_u);
+  int32_t* sched_wo = reinterpret_cast<int32_t*>(host + lay.sched_wo);
+  int32_t* sched_wu = reinterpret_cast<int32_t*>(host + lay.sched_wu);
   RotItem* items = reinterpret_cast<RotItem*>(host + lay.rot_items);
   char* zbuf = reinterpret_cast<char*>(plan) + lay.zbuf;
   int64_t total = 0, rot = 0, zoff = 0;
@@ -995,6 +1094,14 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     int64_t k = 0;
     for (int i : order)
       for (int b = 0; b < lin[i].blocks; ++b) sched_u[k++] = (i << kStackBlockBits) | b;
+    // Wide blocks (16 tiles) for batch 9..32, in phase order and longest K first.
+    int64_t nw = 0;
+    for (int i = 0; i < n_linears; ++i)
+      for (int b = 0; b < (lin[i].T + kWideWaves - 1) / kWideWaves; ++b) sched_wo[nw++] = (i << kStackBlockBits) | b;
+    int64_t kw = 0;
+    for (int i : order)
+      for (int b = 0; b < (lin[i].T + kWideWaves - 1) / kWideWaves; ++b) sched_wu[kw++] = (i << kStackBlockBits) | b;
+    h->total_wide = (int32_t)nw;
     h->n_lin = n_linears;
     h->total_blocks = (int32_t)total;
     h->n_phases = z.n_phases;
@@ -1019,7 +1126,6 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
 extern "C" int tp_stack_rotate(void* plan, int64_t batch, void* stream) {
   if (!plan) return TP_ERR_NULL_POINTER;
   if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
-  if (batch > kSlotMaxBatch) return TP_OK;  // the LDS kernel rotates on the fly
   const char* ro = reinterpret_cast<const char*>(plan) + kStackRO;
   PlanReg reg;
   const int n_rot = plan_lookup(plan, &reg) ? reg.n_rot : 0;
