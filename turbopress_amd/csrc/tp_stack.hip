@@ -752,10 +752,14 @@ __device__ __forceinline__ void wide_unit(const uint2 X, const uint32_t* Mw, con
   }
 }
 
-// Wide block wb of linear L: z rows at z + b * zld (fp16, zero past d).
+// Wide block wb of linear L over 512-column chunks [ch0, ch1): z rows at
+// z + b * zld (fp16, zero past d).  The full K range writes y; a part of it
+// adds its sums into the linear's workspace with device-scope atomics, and
+// the wave that completes a tile's K range (counted per tile) writes y and
+// clears the sums (the split-K protocol of tcq_gemv_tiled_kernel).
 template <int KB, int NS, int NBT>
-__device__ void wide_block(const LinearDesc& L, int wb, const uint16_t* z, int zld, int batch, uint16_t* zl,
-                           const uint32_t* table, uint32_t laneoff, int tid, int wave, int lane) {
+__device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const uint16_t* z, int zld, int batch,
+                           uint16_t* zl, const uint32_t* table, uint32_t laneoff, int tid, int wave, int lane) {
   constexpr int MW = member_words(KB);
   const int r = lane & 15, q = lane >> 4;
   const int t = wb * kWideWaves + wave;
@@ -768,17 +772,18 @@ __device__ void wide_block(const LinearDesc& L, int wb, const uint16_t* z, int z
   float4_t acc[NBT];
 #pragma unroll
   for (int bt = 0; bt < NBT; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
-  uint32_t x1_last = 0;
+  // halo of the range's first unit: word 1 of the previous unit's last segment
+  uint32_t x1_last = ch0 > 0 ? pt[((4 * ch0 * kMaxUnitsPerBlock - 1) * kTileRows + r) * 2 + 1] : 0u;
   {
-    const ZChunk c0 = wide_load_z(zrs, zld, batch, 0, tid);
-    wide_store_z(zl, c0, batch, tid);
+    const ZChunk c0 = wide_load_z(zrs, zld, batch, ch0, tid);
+    wide_store_z(zl + (ch0 & 1) * kWideChunkHalves, c0, batch, tid);
   }
   __syncthreads();
   // Chunk ch: prefetch chunk ch + 1 of z, decode + multiply ch, store the
   // prefetch into the other buffer, one barrier (the next chunk's buffer is
   // full and nobody still reads the one it will overwrite).
   auto body = [&](int ch, const ChunkRegs<MW>& regs) {
-    const bool more = ch + 1 < nch;
+    const bool more = ch + 1 < ch1;
     ZChunk nx;
     if (more) nx = wide_load_z(zrs, zld, batch, ch + 1, tid);
     const uint16_t* zb = zl + (ch & 1) * kWideChunkHalves;
@@ -798,32 +803,58 @@ __device__ void wide_block(const LinearDesc& L, int wb, const uint16_t* z, int z
     if (more) wide_store_z(zl + ((ch + 1) & 1) * kWideChunkHalves, nx, batch, tid);
     __syncthreads();
   };
-  ChunkRegs<MW> ra = load_chunk<MW>(L, pt, mt, 0, q, r);
-  for (int ch = 0; ch < nch; ch += 2) {
-    const ChunkRegs<MW> rb = load_chunk<MW>(L, pt, mt, ch + 1 < nch ? ch + 1 : ch, q, r);
+  ChunkRegs<MW> ra = load_chunk<MW>(L, pt, mt, ch0, q, r);
+  for (int ch = ch0; ch < ch1; ch += 2) {
+    const ChunkRegs<MW> rb = load_chunk<MW>(L, pt, mt, ch + 1 < ch1 ? ch + 1 : ch, q, r);
     body(ch, ra);
-    if (ch + 1 >= nch) break;
-    ra = load_chunk<MW>(L, pt, mt, ch + 2 < nch ? ch + 2 : ch, q, r);
+    if (ch + 1 >= ch1) break;
+    ra = load_chunk<MW>(L, pt, mt, ch + 2 < ch1 ? ch + 2 : ch, q, r);
     body(ch + 1, rb);
   }
+  if (!active) return;
 
-  // Full-K epilogue: lane holds rows 4q..4q+3 of its tile for batch column r.
-  if (active) {
-    const int row0 = t * kTileRows + 4 * q;
+  // Epilogue: lane holds rows 4q..4q+3 of its tile for batch column r.
+  const int row0 = t * kTileRows + 4 * q;
+  float v[NBT][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = row0 + i;
-      if (row >= L.n) continue;
-      const float sc = h2f(gld(L.scales + row));
-      const float bs = L.bias ? h2f(gld(L.bias + row)) : 0.f;
+  for (int bt = 0; bt < NBT; ++bt)
 #pragma unroll
-      for (int bt = 0; bt < NBT; ++bt) {
-        const int nb = bt * 16 + r;
-        if (nb >= batch) continue;
-        uint16_t out = f2h(acc[bt][i] * sc);
-        if (L.bias) out = f2h(h2f(out) + bs);
-        gst(L.y + (size_t)nb * L.ldy + row, out);
-      }
+    for (int i = 0; i < 4; ++i) v[bt][i] = acc[bt][i];
+  if (ch0 > 0 || ch1 < nch) {
+    const int ldws = 16 * NBT;
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) {
+      if (bt * 16 + r >= batch) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) atomicAdd(L.ws + (size_t)(row0 + i) * ldws + bt * 16 + r, v[bt][i]);
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const uint32_t units = (uint32_t)(min(ch1 * kMaxUnitsPerBlock, L.G4) - ch0 * kMaxUnitsPerBlock);
+    uint32_t old = 0;
+    if (lane == 0) old = atomicAdd(L.cnt + t, units);
+    old = (uint32_t)__shfl((int)old, 0, 64);
+    if (old + units != (uint32_t)L.G4) return;
+    // Last contributor: read and clear the sums (also read-modify-write atomics).
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        v[bt][i] = (bt * 16 + r < batch) ? atomicExch(L.ws + (size_t)(row0 + i) * ldws + bt * 16 + r, 0.f) : 0.f;
+    if (lane == 0) atomicExch(L.cnt + t, 0u);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = row0 + i;
+    if (row >= L.n) continue;
+    const float sc = h2f(gld(L.scales + row));
+    const float bs = L.bias ? h2f(gld(L.bias + row)) : 0.f;
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) {
+      const int nb = bt * 16 + r;
+      if (nb >= batch) continue;
+      uint16_t out = f2h(v[bt][i] * sc);
+      if (L.bias) out = f2h(h2f(out) + bs);
+      gst(L.y + (size_t)nb * L.ldy + row, out);
     }
   }
 }
@@ -871,7 +902,8 @@ tcq_stack_wide_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
         __syncthreads();
       }
     }
-    wide_block<KB, NS, NBT>(L, wb, L.z, L.G4 * kChunkCols, batch, zl, table, laneoff, tid, wave, lane);
+    wide_block<KB, NS, NBT>(L, wb, 0, (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock, L.z, L.G4 * kChunkCols,
+                            batch, zl, table, laneoff, tid, wave, lane);
     if (ordered) {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -891,6 +923,79 @@ tcq_stack_wide_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
       atomicExch(&C->exited, 0u);
     }
   }
+}
+
+// One linear at batch 9..32 with its rotated activations already in z
+// (fp16 [batch][zld], zero past d): one workgroup per wide block.
+template <int KB, int NS, int NBT>
+__global__ void __launch_bounds__(kWideThreads)
+tcq_wide_linear_kernel(const LinearDesc L, const uint16_t* __restrict__ z, int zld, int batch,
+                       const uint16_t* __restrict__ codebook, int cps) {
+  __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
+  extern __shared__ __attribute__((aligned(16))) uint16_t zl[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t laneoff = lane_offsets<KB>(lane);
+  const uint32_t cb_lane = gld(codebook + (lane & ((2 << KB) - 1)));
+  build_pair_table_lanes<KB>(table, cb_lane, tid, kWideThreads);
+  __syncthreads();
+  // workgroup (x, y) = (wide block, K part of cps chunks)
+  const int nch = (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock;
+  const int ch0 = (int)blockIdx.y * cps;
+  wide_block<KB, NS, NBT>(L, (int)blockIdx.x, ch0, min(nch, ch0 + cps), z, zld, batch, zl, table, laneoff, tid,
+                          wave, lane);
+}
+
+template <int KB, int NS>
+void launch_wide_linear(const LinearDesc& L, const uint16_t* z, int zld, int batch, const uint16_t* cb,
+                        hipStream_t s) {
+  // Split K until the workgroups cover the CUs (down to one chunk per part;
+  // fewer, longer parts measured slower despite fewer split-K atomics).
+  const int groups = (L.T + kWideWaves - 1) / kWideWaves;
+  const int nch = (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock;
+  const int want = (device_cu_count() + groups - 1) / groups;
+  const int parts = L.ws ? std::max(1, std::min(nch, want)) : 1;
+  const int cps = (nch + parts - 1) / parts;
+  const dim3 grid(groups, (nch + cps - 1) / cps);
+  const size_t zbytes = (size_t)2 * kWideChunkHalves * 2;
+  auto kern = batch <= 16 ? tcq_wide_linear_kernel<KB, NS, 1> : tcq_wide_linear_kernel<KB, NS, 2>;
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)zbytes);
+  hipLaunchKernelGGL(kern, grid, dim3(kWideThreads), zbytes, s, L, z, zld, batch, cb, cps);
+}
+
+int linear_forward_wide(const LinearDesc& Lin, const uint16_t* z, int64_t zld, int64_t batch,
+                        const uint16_t* codebook, int bits, int n_states, void* workspace, int64_t workspace_bytes,
+                        hipStream_t s) {
+  if (batch <= kSlotMaxBatch || batch > 32) return kLinearNotHandled;
+  // split-K sums: fp32 [T * 16 rows][16 * NBT] then one counter per tile
+  LinearDesc L = Lin;
+  const int64_t nbt = batch <= 16 ? 1 : 2;
+  const int64_t sums = (int64_t)L.T * kTileRows * 16 * nbt * 4;
+  if (workspace && workspace_bytes >= sums + (int64_t)L.T * 4 && !((uintptr_t)workspace & 15)) {
+    L.ws = reinterpret_cast<float*>(workspace);
+    L.cnt = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(workspace) + sums);
+  } else {
+    L.ws = nullptr;
+    L.cnt = nullptr;
+  }
+  switch (bits * 100 + n_states) {
+    case 204: launch_wide_linear<2, 4>(L, z, (int)zld, (int)batch, codebook, s); break;
+    case 208: launch_wide_linear<2, 8>(L, z, (int)zld, (int)batch, codebook, s); break;
+    case 216: launch_wide_linear<2, 16>(L, z, (int)zld, (int)batch, codebook, s); break;
+    case 264: launch_wide_linear<2, 64>(L, z, (int)zld, (int)batch, codebook, s); break;
+    case 304: launch_wide_linear<3, 4>(L, z, (int)zld, (int)batch, codebook, s); break;
+    case 308: launch_wide_linear<3, 8>(L, z, (int)zld, (int)batch, codebook, s); break;
+    case 316: launch_wide_linear<3, 16>(L, z, (int)zld, (int)batch, codebook, s); break;
+    case 364: launch_wide_linear<3, 64>(L, z, (int)zld, (int)batch, codebook, s); break;
+    case 404: launch_wide_linear<4, 4>(L, z, (int)zld, (int)batch, codebook, s); break;
+    case 408: launch_wide_linear<4, 8>(L, z, (int)zld, (int)batch, codebook, s); break;
+    case 416: launch_wide_linear<4, 16>(L, z, (int)zld, (int)batch, codebook, s); break;
+    case 464: launch_wide_linear<4, 64>(L, z, (int)zld, (int)batch, codebook, s); break;
+    default: return TP_ERR_UNSUPPORTED_STATES;
+  }
+  return launch_status();
 }
 
 inline int slot_batch(int64_t batch) { return batch <= 4 ? 4 : 8; }

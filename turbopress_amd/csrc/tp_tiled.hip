@@ -528,6 +528,15 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
   // Batch <= 8 runs the one-pass kernel (tp_linear.hip) when it applies.
   const int fast = linear_forward_fast(ls, n_lin, batch, codebook, bits, n_states, (hipStream_t)stream);
   if (fast != kLinearNotHandled) return fast;
+  // Batch 9..32 on rotated activations: 16-tile blocks through LDS (tp_stack.hip).
+  if (!rot && batch > 8) {
+    for (int i = 0; i < n_lin; ++i) {
+      const int st = linear_forward_wide(a.lin[i], ls[i].x, ls[i].ldx, batch, codebook, bits, n_states,
+                                         ls[i].workspace, ls[i].workspace_bytes, (hipStream_t)stream);
+      if (st) return st;
+    }
+    return TP_OK;
+  }
   a.total_blocks = (int32_t)total_blocks;
   const int wg_per_cu = nbt == 1 ? 2 : 1;
   int grid = (int)(total_blocks < (int64_t)cus * wg_per_cu ? total_blocks : (int64_t)cus * wg_per_cu);

@@ -549,6 +549,15 @@ constexpr int kLinearNotHandled = 1 << 20;
 int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
                         int bits, int n_states, hipStream_t s);
 
+// Batch 9..32 decode-GEMV of one linear whose activations are already
+// rotated (z fp16 [batch][zld], zero past d), in 16-tile blocks, K split
+// across workgroups through the workspace (tp_gemv_workspace_bytes) when one
+// is given (tp_stack.hip).  Returns a status, or kLinearNotHandled for
+// other batches.
+int linear_forward_wide(const LinearDesc& L, const uint16_t* z, int64_t zld, int64_t batch,
+                        const uint16_t* codebook, int bits, int n_states, void* workspace, int64_t workspace_bytes,
+                        hipStream_t s);
+
 // ---------------------------------------------------------------------------
 // host-side geometry
 // ---------------------------------------------------------------------------
