@@ -28,6 +28,10 @@ duration, timed with HIP events around back-to-back launches on the stream
 they run on.  ``read_reference`` is a plain streaming read of the step's
 byte count (``tp_read_probe``): the read bandwidth the box reaches with no
 compute, i.e. the practical ceiling the kernel is compared against.
+``batch32`` (comparison runs only) is the batch >= 16 path, the MFMA
+skinny GEMM of BASELINE.json configs[4]: the same stack at batch 32 and the
+gate / down shapes per linear at batch 32, as time, TFLOP/s and fraction of
+the 2.5 PFLOP/s dense fp16 MFMA peak.
 ``encoder`` (comparison runs only) times the compress-time TCQ Viterbi
 search on a gate_proj-sized matrix; its CPU comparison sits in the
 CPU-baseline leg.
@@ -47,6 +51,7 @@ from pathlib import Path
 import torch
 
 HBM_PEAK_GBPS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 N_LAYERS = 36
 BITS = 3
 N_STATES = 64
@@ -244,6 +249,39 @@ def cpu_encoder_baseline(sample) -> dict:
             "codes_match_gpu": bool(torch.equal(gpu_codes, ref[0]))}
 
 
+def batch32_reference(layers, steps: int, warmup: int) -> dict:
+    """The batch >= 16 path (MFMA skinny GEMM): the same 36-layer stack at
+    batch 32 (one rotation launch + one wide-kernel launch), and the c4
+    per-linear shapes (gate 2560->9728, down 9728->2560) at batch 32 through
+    PackedTCQLinear.forward, each cycling over the 36 layers' copies so no
+    launch reads cached weights.  Achieved TFLOP/s = 2*B*n*d / time."""
+    dev = layers[0]["q_proj"].scales.device
+    batch = 32
+    from turbopress_amd.synthetic import make_activation
+    inputs = []
+    for li in range(len(layers)):
+        inputs.append({g: make_activation(batch, d, seed=5000 + 10 * li + k).to(dev)
+                       for k, (g, d) in enumerate((("attn", 2560), ("o", 4096), ("mlp", 2560), ("down", 9728)))})
+    weights = sum(m.out_features * m.in_features for mods in layers for m in mods.values())
+    stack = make_stack(layers, inputs, ordered=False)
+    ms, _, _ = time_graph(stack.run, steps, warmup)
+    us_gemv = time_gemv_kernel(stack, steps, warmup)
+    tf = 2 * batch * weights / (us_gemv * 1e-6) / 1e12
+    out = {"batch": batch, "stack_us_per_step": round(ms * 1e3, 2), "stack_gemv_us": round(us_gemv, 2),
+           "stack_gemv_tflops": round(tf, 1), "stack_gemv_mfma_frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4)}
+    for name, g in (("gate_proj", "mlp"), ("down_proj", "down")):
+        def run(name=name, g=g):
+            for mods, xs in zip(layers, inputs):
+                mods[name](xs[g])
+        ms_l, _, _ = time_graph(run, max(5, steps // 10), 3)
+        us = ms_l * 1e3 / len(layers)
+        m = layers[0][name]
+        tfl = 2 * batch * m.out_features * m.in_features / (us * 1e-6) / 1e12
+        out[name] = {"us_per_linear": round(us, 2), "tflops": round(tfl, 2),
+                     "mfma_frac": round(tfl / MFMA_FP16_PEAK_TFLOPS, 4)}
+    return out
+
+
 def cpu_baseline(budget_s: float):
     """The reference's CPU tiled path (oracle restatement), one Qwen3-4B layer
     at k=3, B=1, repeated until ~budget_s of CPU work, scaled to 36 layers."""
@@ -341,8 +379,11 @@ def main() -> int:
         log(f"device copy {args.copy_mib} MiB: {copy_ref['gbps']} GB/s (read + write)")
     read_ref = read_reference(nbytes)
     log(f"streaming read of {nbytes / 1e9:.4f} GB: {read_ref['us']} us, {read_ref['gbps']} GB/s")
-    enc, enc_sample = None, None
+    enc, enc_sample, b32 = None, None, None
     if not args.only_primary:
+        b32 = batch32_reference(layers, args.steps, args.warmup)
+        log(f"batch 32: stack {b32['stack_gemv_us']} us/GEMV launch, {b32['stack_gemv_tflops']} TFLOP/s; "
+            f"gate {b32['gate_proj']['us_per_linear']} us, down {b32['down_proj']['us_per_linear']} us per linear")
         enc, enc_sample = encoder_reference()
         log(f"TCQ Viterbi encoder, {enc['rows']}x{enc['dim']}: GPU {enc['gpu_us']} us")
     cpu = None
@@ -375,6 +416,7 @@ def main() -> int:
         "executors": extra,
         "copy_reference": copy_ref,
         "read_reference": read_ref,
+        "batch32": b32,
         "encoder": enc,
         "cpu_baseline": cpu,
     }
