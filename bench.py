@@ -327,6 +327,8 @@ def main() -> int:
                     help="size of the device copy reported as copy_reference (0: skip)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only-primary", action="store_true", help="skip the comparison executors")
+    ap.add_argument("--only-batch32", action="store_true",
+                    help="run only the batch-32 leg (profiling the MFMA path) and print its figures")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: the packed-TCQ decode path is built and measured "
@@ -342,6 +344,9 @@ def main() -> int:
     layers, inputs = build_layers(dev)
     nbytes = step_bytes(layers)
     log(f"{nbytes / 1e9:.4f} GB per step")
+    if args.only_batch32:
+        print(json.dumps({"batch32": batch32_reference(layers, args.steps, args.warmup)}), flush=True)
+        return 0
 
     stack = make_stack(layers, inputs, ordered=False)
     ms, ms_wall, _ = time_graph(stack.run, args.steps, args.warmup)
