@@ -101,3 +101,84 @@ def decode_graph(model, prompt_ids, n_new: int, max_len: int, warmup: int = 3):
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
     return out, timed / dt if dt > 0 and timed else float("inf")
+
+
+# ---------------------------------------------------------------------------
+# command line: the reference's scripts/graph_decode_bench.py for this build
+# ---------------------------------------------------------------------------
+# Decoder shapes of the models the reference benchmarks and configures
+# (random weights only: nothing is downloaded).
+SYNTHETIC = {
+    "smollm2-135m": ("llama", dict(vocab_size=49152, hidden_size=576, intermediate_size=1536,
+                                   num_hidden_layers=30, num_attention_heads=9, num_key_value_heads=3,
+                                   tie_word_embeddings=True, max_position_embeddings=2048)),
+    "qwen3-0.6b": ("qwen3", dict(vocab_size=151936, hidden_size=1024, intermediate_size=3072,
+                                 num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8,
+                                 head_dim=128, tie_word_embeddings=True, max_position_embeddings=2048)),
+}
+
+
+def synthetic_config(name: str):
+    """A transformers config of one of the SYNTHETIC decoder shapes."""
+    from transformers import LlamaConfig, Qwen3Config
+    kind, kw = SYNTHETIC[name]
+    cls = LlamaConfig if kind == "llama" else Qwen3Config
+    return cls(torch_dtype="float16", **kw)
+
+
+def main(argv=None) -> int:
+    """Greedy decode tokens/s of a packed model, eager and with one captured
+    decode step replayed per token (graph_decode_bench.py:121-158), optionally
+    beside the dense fp16 model of the same shape.  Prints one JSON line."""
+    import argparse
+    import json
+    import tempfile
+
+    from turbopress_amd.artifact import load_packed_model
+    from turbopress_amd.synthetic import write_synthetic_artifact
+
+    ap = argparse.ArgumentParser(description=main.__doc__.splitlines()[0])
+    src = ap.add_mutually_exclusive_group(required=True)
+    src.add_argument("--artifact", help="format-v1 artifact directory")
+    src.add_argument("--synthetic", choices=sorted(SYNTHETIC), help="seeded synthetic model of this shape")
+    ap.add_argument("--bits", type=int, default=3)
+    ap.add_argument("--n-states", type=int, default=64)
+    ap.add_argument("--mode", default="hip", choices=("hip", "triton", "cached"))
+    ap.add_argument("--prompt-len", type=int, default=16)
+    ap.add_argument("--new-tokens", type=int, default=128)
+    ap.add_argument("--fp16-baseline", action="store_true", help="also time the dense fp16 model")
+    args = ap.parse_args(argv)
+
+    with tempfile.TemporaryDirectory() as tmp:
+        root = args.artifact
+        if args.synthetic:
+            root = tmp
+            write_synthetic_artifact(root, synthetic_config(args.synthetic), bits=args.bits,
+                                     n_states=args.n_states, seed=0)
+        model, meta = load_packed_model(root, device="cuda", mode=args.mode)
+    vocab = model.config.vocab_size
+    prompt = torch.randint(0, vocab, (1, args.prompt_len), generator=torch.Generator().manual_seed(0)).cuda()
+    max_len = args.prompt_len + args.new_tokens + 8
+    toks_e, tps_e = decode_eager(model, prompt, args.new_tokens, max_len)
+    toks_g, tps_g = decode_graph(model, prompt, args.new_tokens, max_len)
+    out = {"model": args.synthetic or str(args.artifact), "mode": args.mode, "bits": int(meta.get("bits", args.bits)),
+           "n_states": int(meta["n_states"]), "prompt_len": args.prompt_len, "new_tokens": args.new_tokens,
+           "eager_tok_s": round(tps_e, 1), "graph_tok_s": round(tps_g, 1), "greedy_tokens_match": toks_e == toks_g}
+    if args.fp16_baseline:
+        from transformers import AutoConfig, AutoModelForCausalLM
+        del model
+        torch.cuda.empty_cache()
+        torch.manual_seed(0)
+        config = (synthetic_config(args.synthetic) if args.synthetic
+                  else AutoConfig.from_pretrained(f"{args.artifact}/hf_config"))
+        dense = AutoModelForCausalLM.from_config(config)
+        dense = dense.to(device="cuda", dtype=torch.float16).eval()
+        out["fp16_eager_tok_s"] = round(decode_eager(dense, prompt, args.new_tokens, max_len)[1], 1)
+        out["fp16_graph_tok_s"] = round(decode_graph(dense, prompt, args.new_tokens, max_len)[1], 1)
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    import sys
+    sys.exit(main())
