@@ -91,6 +91,42 @@ def test_qwen3_4b_forward_matches_tiled_oracle(cuda, name):
     assert O.max_rel(y, O.tiled_forward(payload_numpy(p), x.numpy())) <= GEMV_TOL
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("name", ["gate_proj", "down_proj"])
+def test_c3_mlp_rates_and_batches(cuda, name, bits):
+    """Config 3: Qwen3-4B MLP shapes at k = 2, 3, 4 and batch 1, 4, 8 (one-pass
+    kernel at 1 and 4 where the input fits, split-K kernel otherwise), each
+    batch a separate forward checked against one oracle evaluation."""
+    from turbopress_amd.runtime import PackedTCQLinear
+    d, n = QWEN3_4B_LAYER[name]
+    p = make_payload(n, d, bits, 64, seed=40 + bits)
+    lin = PackedTCQLinear(p, mode="hip")
+    xs = [make_activation(b, d, seed=10 * bits + b) for b in (1, 4, 8)]
+    ref = O.tiled_forward(payload_numpy(p), np.concatenate([x.numpy() for x in xs]))
+    r0 = 0
+    for x in xs:
+        y = lin(x.to(cuda)).float().cpu().numpy()
+        assert O.max_rel(y, ref[r0:r0 + x.shape[0]]) <= GEMV_TOL, (name, bits, x.shape[0])
+        r0 += x.shape[0]
+
+
+@pytest.mark.parametrize("name", ["gate_proj", "down_proj"])
+def test_c4_batch32(cuda, name):
+    """Config 4: down / gate at batch 32, k=3 (rotation + wide kernel with
+    split-K sums in the workspace), twice in a row (the workspace returns to
+    zero)."""
+    from turbopress_amd.runtime import PackedTCQLinear
+    d, n = QWEN3_4B_LAYER[name]
+    p = make_payload(n, d, 3, 64, seed=77)
+    lin = PackedTCQLinear(p, mode="hip")
+    x = make_activation(32, d, seed=5)
+    ref = O.tiled_forward(payload_numpy(p), x.numpy())
+    for _ in range(2):
+        y = lin(x.to(cuda)).float().cpu().numpy()
+        assert O.max_rel(y, ref) <= GEMV_TOL
+    assert int(lin._gemv_ws.count_nonzero()) == 0
+
+
 def test_workspace_returns_to_zero_and_calls_repeat(cuda):
     from turbopress_amd.runtime import PackedTCQLinear
     p = make_payload(2560, 9728, 3, 64, seed=5, bias=True)
