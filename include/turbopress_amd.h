@@ -247,9 +247,9 @@ int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears, int bits,
                        int64_t batch, void* plan, int64_t plan_bytes);
 
 /* Run every linear of the plan (y = PackedTCQLinear.forward(x) for each, as
- * tp_packed_linear_forward computes it): for batch <= 8 one small launch
- * rotates every input into the plan's z buffer and ONE persistent launch
- * runs all GEMVs; for batch 9..32 one persistent launch does both.  With
+ * tp_packed_linear_forward computes it): one small launch rotates every
+ * input into the plan's z buffer and ONE persistent launch runs all GEMVs
+ * (batch <= 8: the slot kernel; 9..32: the wide kernel).  With
  * ordered != 0 a linear of phase p starts only after all linears of phase
  * p-1 finished.  The plan's counters return to zero after each run, so one
  * plan serves any number of runs or graph replays on one stream (runs that
@@ -261,10 +261,10 @@ int tp_stack_run(void* plan, int64_t batch, const uint16_t* codebook, int bits,
                  int n_states, int ordered, int64_t total_blocks, void* stream);
 
 /* The two launches of tp_stack_run, for callers that schedule them apart:
- * tp_stack_rotate fills the plan's z buffer from the current inputs (a no-op
- * for batch > 8); tp_stack_gemv runs the GEMVs from it (batch <= 8) or from
- * the inputs directly (batch > 8).  A tp_stack_gemv run after new inputs
- * were written needs a tp_stack_rotate in between on the same stream. */
+ * tp_stack_rotate fills the plan's z buffer from the current inputs;
+ * tp_stack_gemv runs the GEMVs from it.  A tp_stack_gemv run after new
+ * inputs were written needs a tp_stack_rotate in between on the same
+ * stream. */
 int tp_stack_rotate(void* plan, int64_t batch, void* stream);
 int tp_stack_gemv(void* plan, int64_t batch, const uint16_t* codebook, int bits,
                   int n_states, int ordered, int64_t total_blocks, void* stream);

@@ -38,7 +38,7 @@ def _check(payloads, stack):
 @pytest.mark.parametrize("batch", [1, 2, 3, 5, 8, 12, 20])
 def test_stack_matches_oracle(cuda, ordered, batch):
     """Batch 1-2 / 3-4 / 5-8: slot kernel with 8 / 4 / 2 slots per z load;
-    9-16 / 17-32: LDS-staged kernel with one / two batch tiles."""
+    9-16 / 17-32: wide kernel with one / two batch tiles."""
     payloads, stack = _build(cuda, MIXED, batch, ordered=ordered, bias=True)
     stack.run()
     torch.cuda.synchronize()
@@ -65,7 +65,7 @@ def test_stack_k2_and_repeat_runs_reset_counters(cuda):
 
 @pytest.mark.parametrize("batch", [1, 4, 8, 12])
 def test_stack_k4(cuda, batch):
-    """4 bits/weight: slot kernel (batch <= 8) and LDS-staged kernel."""
+    """4 bits/weight: slot kernel (batch <= 8) and wide kernel."""
     payloads, stack = _build(cuda, MIXED, batch, bits=4, bias=True)
     stack.run()
     torch.cuda.synchronize()

@@ -63,7 +63,7 @@ GEMV_CASES = [
     (2560, 9728, 4, 64, 3),
     (130, 200, 4, 16, 2),
     (1024, 2560, 4, 64, 8),      # k=4: split-K kernel
-    (300, 512, 4, 8, 20),        # k=4: LDS-staged batches
+    (300, 512, 4, 8, 20),        # k=4: wide kernel (rotated input)
 ]
 
 
