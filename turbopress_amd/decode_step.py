@@ -99,7 +99,7 @@ class LinearStack:
 
     def gemv(self) -> list:
         """Second launch of run(): every GEMV, from the z buffer the last
-        rotate() filled (batch <= 8) or from the inputs (batch > 8)."""
+        rotate() filled."""
         st = _lib.lib().tp_stack_gemv(self.plan.data_ptr(), self.batch, self.codebook.data_ptr(),
                                       self.bits, self.n_states, int(self.ordered), self.total_blocks,
                                       hk.current_stream_ptr(self.plan.device))
