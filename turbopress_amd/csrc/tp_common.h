@@ -16,6 +16,10 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include <mutex>
+#include <set>
+#include <utility>
+
 #include "../../include/turbopress_amd.h"
 
 namespace tp {
@@ -107,6 +111,34 @@ inline int device_cu_count() {
     cached[dev] = cus;
   }
   return cached[dev];
+}
+
+// Largest LDS allocation of one workgroup on the current device (cached per
+// device; 64 KiB if the query fails).
+inline int device_max_lds() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
+  if (!cached[dev]) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+      v = 64 * 1024;
+    cached[dev] = v;
+  }
+  return cached[dev];
+}
+
+// Let kernel `fn` (with `static_bytes` of static LDS) take the rest of the
+// device's LDS as dynamic LDS.  Done once per kernel and device; later
+// launches make no runtime call for it.
+inline void allow_dynamic_lds(const void* fn, int static_bytes) {
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.insert({fn, dev}).second)
+    (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, device_max_lds() - static_bytes);
 }
 
 inline int launch_status() {

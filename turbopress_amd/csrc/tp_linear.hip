@@ -421,25 +421,10 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
 // ---------------------------------------------------------------------------
 namespace {
 
-// Largest LDS allocation of one workgroup on the current device (cached).
-int device_max_lds() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 64 * 1024;
-  if (!cached[dev]) {
-    int v = 0;
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
-      v = 64 * 1024;
-    cached[dev] = v;
-  }
-  return cached[dev];
-}
-
 template <int KB, int NS, int SB, bool ROT>
 void launch_linear(const LinArgs& a, int grid, size_t dyn, hipStream_t s) {
   auto kern = a.n_part > 1 ? tcq_linear_kernel<KB, NS, SB, ROT, true> : tcq_linear_kernel<KB, NS, SB, ROT, false>;
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)dyn);
+  allow_dynamic_lds(reinterpret_cast<const void*>(kern), kTableBytes + 256);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kLinThreads), dyn, s, a);
 }
 

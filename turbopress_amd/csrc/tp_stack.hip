@@ -960,8 +960,7 @@ void launch_wide_linear(const LinearDesc& L, const uint16_t* z, int zld, int bat
   const dim3 grid(groups, (nch + cps - 1) / cps);
   const size_t zbytes = (size_t)2 * kWideChunkHalves * 2;
   auto kern = batch <= 16 ? tcq_wide_linear_kernel<KB, NS, 1> : tcq_wide_linear_kernel<KB, NS, 2>;
-  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)zbytes);
+  allow_dynamic_lds(reinterpret_cast<const void*>(kern), kTableBytes + 256);
   hipLaunchKernelGGL(kern, grid, dim3(kWideThreads), zbytes, s, L, z, zld, batch, cb, cps);
 }
 
@@ -1042,13 +1041,11 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
     const size_t zbytes = (size_t)2 * kWideChunkHalves * 2;
     if (batch <= 16) {
       auto kern = tcq_stack_wide_kernel<KB, NS, 1>;
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)zbytes);
+      allow_dynamic_lds(reinterpret_cast<const void*>(kern), kTableBytes + 256);
       hipLaunchKernelGGL(kern, dim3(grid), dim3(kWideThreads), zbytes, s, ro, plan, cb, ordered, spin_limit);
     } else {
       auto kern = tcq_stack_wide_kernel<KB, NS, 2>;
-      (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)zbytes);
+      allow_dynamic_lds(reinterpret_cast<const void*>(kern), kTableBytes + 256);
       hipLaunchKernelGGL(kern, dim3(grid), dim3(kWideThreads), zbytes, s, ro, plan, cb, ordered, spin_limit);
     }
   }
