@@ -136,3 +136,24 @@ def test_graph_decode_matches_eager(cuda, tiny_artifact):
     toks_g, _ = decode_graph(model, ids, n_new, max_len)
     assert len(toks_e) == len(toks_g) == n_new
     assert toks_e == toks_g
+
+
+@pytest.mark.gpu
+def test_fused_shared_input_projections_match(cuda, tiny_artifact):
+    """q/k/v and gate/up joined into one launch per group: same logits (to
+    the GEMV tolerance) and the same greedy tokens, eager and graph-replayed."""
+    from turbopress_amd.decode_step import fuse_shared_input_projections
+    from turbopress_amd.graph_decode import decode_eager, decode_graph
+    ids = torch.randint(0, 1024, (1, 8), generator=torch.Generator().manual_seed(2)).to(cuda)
+    model, _ = load_packed_model(tiny_artifact, device="cuda", mode="hip")
+    with torch.inference_mode():
+        ref = model(input_ids=ids).logits.float()
+    toks_ref, _ = decode_eager(model, ids, 12, 32)
+    assert fuse_shared_input_projections(model) == 2 * len(model.model.layers)
+    with torch.inference_mode():
+        fused = model(input_ids=ids).logits.float()
+    rel = ((fused - ref).abs().max() / ref.abs().max()).item()
+    assert rel < 5e-3, rel
+    toks_e, _ = decode_eager(model, ids, 12, 32)
+    toks_g, _ = decode_graph(model, ids, 12, 32)
+    assert toks_e == toks_ref and toks_g == toks_ref

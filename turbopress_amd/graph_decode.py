@@ -147,6 +147,8 @@ def main(argv=None) -> int:
     ap.add_argument("--prompt-len", type=int, default=16)
     ap.add_argument("--new-tokens", type=int, default=128)
     ap.add_argument("--fp16-baseline", action="store_true", help="also time the dense fp16 model")
+    ap.add_argument("--fuse", action="store_true",
+                    help="one launch per shared-input group (q/k/v, gate/up) instead of per projection")
     args = ap.parse_args(argv)
 
     with tempfile.TemporaryDirectory() as tmp:
@@ -156,12 +158,15 @@ def main(argv=None) -> int:
             write_synthetic_artifact(root, synthetic_config(args.synthetic), bits=args.bits,
                                      n_states=args.n_states, seed=0)
         model, meta = load_packed_model(root, device="cuda", mode=args.mode)
+    if args.fuse:
+        from turbopress_amd.decode_step import fuse_shared_input_projections
+        fuse_shared_input_projections(model)
     vocab = model.config.vocab_size
     prompt = torch.randint(0, vocab, (1, args.prompt_len), generator=torch.Generator().manual_seed(0)).cuda()
     max_len = args.prompt_len + args.new_tokens + 8
     toks_e, tps_e = decode_eager(model, prompt, args.new_tokens, max_len)
     toks_g, tps_g = decode_graph(model, prompt, args.new_tokens, max_len)
-    out = {"model": args.synthetic or str(args.artifact), "mode": args.mode, "bits": int(meta.get("bits", args.bits)),
+    out = {"model": args.synthetic or str(args.artifact), "mode": args.mode, "fused_groups": args.fuse, "bits": int(meta.get("bits", args.bits)),
            "n_states": int(meta["n_states"]), "prompt_len": args.prompt_len, "new_tokens": args.new_tokens,
            "eager_tok_s": round(tps_e, 1), "graph_tok_s": round(tps_g, 1), "greedy_tokens_match": toks_e == toks_g}
     if args.fp16_baseline:

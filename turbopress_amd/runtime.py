@@ -133,6 +133,8 @@ class PackedTCQLinear(nn.Module):
         self.register_buffer("tiled_packed", None)
         self.register_buffer("_gemv_ws", None, persistent=False)
         self._tiled_geo = None
+        self._group = None       # SharedInputGroup this layer belongs to (decode_step)
+        self._group_index = 0
         if self.mode == "hip":
             if self.bits in hk.TILED_BITS:
                 # Load-time re-tile into the MFMA kernel's layout, still at the
@@ -188,6 +190,8 @@ class PackedTCQLinear(nn.Module):
             raise ValueError(f"expected last dim {self.in_features}, got {x.shape[-1]}")
         if not x.is_cuda:
             raise RuntimeError("PackedTCQLinear runs on a ROCm GPU; move the input to CUDA")
+        if self._group is not None:
+            return self._group.run(self._group_index, x)
         if self.mode == "cached":
             y = F.linear(x.to(torch.float16), self._w_cache)
             if self.bias is not None:
