@@ -233,8 +233,8 @@ typedef struct tp_stack_linear {
 } tp_stack_linear;
 
 /* Bytes of the device plan of these linears at this batch (0 when invalid):
- * descriptors, schedules, counters and, for batch <= 8, the buffer of
- * rotated activations (batch * ceil(d/256)*256 fp16 per linear).  Host only. */
+ * descriptors, schedules, counters and the buffer of rotated activations
+ * (batch * ceil(d/256)*256 fp16 per linear).  Host only. */
 int64_t tp_stack_plan_bytes(const tp_stack_linear* linears, int n_linears, int bits, int64_t batch);
 
 /* Validate the linears and write the plan (descriptors, block prefix sums,
@@ -249,7 +249,7 @@ int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears, int bits,
 /* Run every linear of the plan (y = PackedTCQLinear.forward(x) for each, as
  * tp_packed_linear_forward computes it): one small launch rotates every
  * input into the plan's z buffer and ONE persistent launch runs all GEMVs
- * (batch <= 8: the slot kernel; 9..32: the wide kernel).  With
+ * (batch <= 4: the slot kernel; 5..32: the wide kernel).  With
  * ordered != 0 a linear of phase p starts only after all linears of phase
  * p-1 finished.  The plan's counters return to zero after each run, so one
  * plan serves any number of runs or graph replays on one stream (runs that

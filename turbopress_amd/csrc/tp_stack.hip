@@ -16,22 +16,23 @@
 //     phase p-1 has finished (bounded wait; on timeout the plan's error flag
 //     is set and the block proceeds, so the kernel always terminates).
 //
-// Batch <= 8 (the decode case) runs two kernels:
+// A run is two kernels:
 //   1. tcq_stack_rotate_kernel: z = blockFWHT(x * rot_scale) / sqrt(hb) of
 //      every linear into the plan's z buffer (fp16, zero past d) -- a few
-//      MB, read back from L2/MALL;
-//   2. tcq_stack_slot_kernel: a wave streams its tile's path/member words
-//      and z with buffer loads, two units ahead, and never synchronises with
-//      the other waves inside a block.  At batch <= 8 only `batch` of the 16
-//      MFMA B columns carry data, so the columns are split into 16/SB "slots"
-//      of SB batch rows: one 16-byte z load per lane feeds 16/SB MFMAs (MFMA
-//      i reads its activations from slot i % (16/SB) and accumulates into its
-//      own accumulator); the valid column of each accumulator is summed
-//      across slots once per block.  The LDS then only serves the codebook
-//      pair table, whose lookups bound the kernel's issue rate.
-// Batch 9..32 runs tcq_stack_wide_kernel after the same rotation launch:
-// 16-wave workgroups stage the rotated activations through LDS in 512-column
-// chunks (double buffered) and every wave reads them as MFMA B operands.
+//      MB at batch 1, read back from L2/MALL;
+//   2. batch <= 4 (the decode case): tcq_stack_slot_kernel: a wave streams
+//      its tile's path/member words and z with buffer loads, three units
+//      ahead, and never synchronises with the other waves inside a block.
+//      Only `batch` of the 16 MFMA B columns carry data, so the columns are
+//      split into 16/SB "slots" of SB batch rows: one 16-byte z load per
+//      lane feeds 16/SB MFMAs (MFMA i reads its activations from slot
+//      i % (16/SB) and accumulates into its own accumulator); the valid
+//      column of each accumulator is summed across slots once per block.
+//      The LDS then only serves the codebook pair table, whose lookups bound
+//      the kernel's issue rate.
+//      Batch 5..32: tcq_stack_wide_kernel: 16-wave workgroups stage the
+//      rotated activations through LDS in 512-column chunks (double
+//      buffered) and every wave reads them as MFMA B operands.
 #include "tp_tiled_common.h"
 #include "tp_slot.h"
 
@@ -46,7 +47,11 @@ namespace tp {
 constexpr int kStackMaxPhases = 4096;
 constexpr int kStackMaxLinears = 4096;       // schedule entries: (linear << 20) | block
 constexpr int kStackBlockBits = 20;
-constexpr int kSlotMaxBatch = 8;             // batches up to this use the slot kernel
+// Batches up to this use the slot kernel (4 batch rows per slot); larger ones
+// the wide kernel, which at batch 8 measured 371 us per Qwen3-4B step
+// against 475 us for 2 slots of 8 rows (whose z registers leave room for only
+// one unit of loads in flight), and at batch 5 about the same.
+constexpr int kSlotMaxBatch = 4;
 
 // Plan layout (device memory):
 //   [0, 64)             StackCounters  -- written by the kernels (atomics)
@@ -55,7 +60,7 @@ constexpr int kSlotMaxBatch = 8;             // batches up to this use the slot 
 //                       lphase[n_lin], pblocks[n_phases], sched_ordered[total],
 //                       sched_unordered[total]  -- read-only
 //   [pdone, ...)        pdone[n_phases] -- written by the kernel (atomics)
-//   [zbuf, ...)         rotated activations, batch <= 8 plans only
+//   [zbuf, ...)         rotated activations
 // The read-only part is passed as a separate const __restrict__ argument so
 // its loads go through the scalar cache into SGPRs.
 struct StackCounters {
@@ -73,7 +78,7 @@ struct StackInfo {
   int32_t n_rot;          // rotation tiles (batch * 4096-column tiles per linear) when the plan has a z buffer
   int32_t min_g4;         // shortest K of the plan in 256-column units
   int64_t zbuf_bytes;
-  int32_t total_wide;     // wide blocks (16 tiles x full K) of the batch 9..32 kernel
+  int32_t total_wide;     // wide blocks (16 tiles x full K) of the batch 5..32 kernel
   int32_t reserved;
 };
 
@@ -192,7 +197,7 @@ __device__ inline void wait_phase(const StackRO& P, uint32_t* pdone, StackCounte
 }
 
 // ---------------------------------------------------------------------------
-// 1. rotation of every linear's input into the plan's z buffer (batch <= 8)
+// 1. rotation of every linear's input into the plan's z buffer
 // ---------------------------------------------------------------------------
 // One workgroup of 256 threads transforms a tile of up to 4096 columns of
 // one batch row (tiles start at multiples of 4096, so a Hadamard block of at
@@ -342,7 +347,7 @@ tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
 }
 
 // ---------------------------------------------------------------------------
-// 2. slot kernel (batch <= 8)
+// 2. slot kernel (batch <= 4)
 // ---------------------------------------------------------------------------
 
 // Read-only state of one wave of the slot kernel.
@@ -655,7 +660,7 @@ tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
 }
 
 // ---------------------------------------------------------------------------
-// 3. wide kernel (batch 9..32)
+// 3. wide kernel (stack: batch 5..32; one linear: batch 9..32)
 // ---------------------------------------------------------------------------
 // One workgroup of 16 waves per CU takes *wide blocks* (16 row tiles x the
 // full K of one linear) by ticket; wave w owns tile w.  The linear's rotated
@@ -967,7 +972,7 @@ void launch_wide_linear(const LinearDesc& L, const uint16_t* z, int zld, int bat
 int linear_forward_wide(const LinearDesc& Lin, const uint16_t* z, int64_t zld, int64_t batch,
                         const uint16_t* codebook, int bits, int n_states, void* workspace, int64_t workspace_bytes,
                         hipStream_t s) {
-  if (batch <= kSlotMaxBatch || batch > 32) return kLinearNotHandled;
+  if (batch <= 8 || batch > 32) return kLinearNotHandled;
   // split-K sums: fp32 [T * 16 rows][16 * NBT] then one counter per tile
   LinearDesc L = Lin;
   const int64_t nbt = batch <= 16 ? 1 : 2;
@@ -997,7 +1002,6 @@ int linear_forward_wide(const LinearDesc& Lin, const uint16_t* z, int64_t zld, i
   return launch_status();
 }
 
-inline int slot_batch(int64_t batch) { return batch <= 4 ? 4 : 8; }
 
 // Each plan initialised in this process with a slot-kernel batch: its
 // rotation tile count, blocks, batch and layout offsets.  A plan the process
@@ -1024,17 +1028,12 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
   const int cus = device_cu_count();
   if (batch <= kSlotMaxBatch) {
     const int grid = (int)(total_blocks < (int64_t)cus * 2 ? total_blocks : (int64_t)cus * 2);
-    const int sb = slot_batch(batch);
     PlanArgs pa = {0, 0, 0, 0};
     PlanReg reg;
     if (plan_lookup(plan, &reg) && reg.batch == batch && reg.total == total_blocks)
       pa = {reg.lin_off, ordered ? reg.sched_o_off : reg.sched_u_off, reg.total, reg.batch};
-    if (sb == 4)
-      hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 4>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
-                         ordered, spin_limit, pa);
-    else
-      hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 8>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
-                         ordered, spin_limit, pa);
+    hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 4>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
+                       ordered, spin_limit, pa);
   } else {
     // one 16-wave workgroup per CU (64 KiB table + two 32 KiB z chunks)
     const int grid = (int)(total_blocks < (int64_t)cus ? total_blocks : (int64_t)cus);
@@ -1196,7 +1195,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     int64_t k = 0;
     for (int i : order)
       for (int b = 0; b < lin[i].blocks; ++b) sched_u[k++] = (i << kStackBlockBits) | b;
-    // Wide blocks (16 tiles) for batch 9..32, in phase order and longest K first.
+    // Wide blocks (16 tiles) for batch 5..32, in phase order and longest K first.
     int64_t nw = 0;
     for (int i = 0; i < n_linears; ++i)
       for (int b = 0; b < (lin[i].T + kWideWaves - 1) / kWideWaves; ++b) sched_wo[nw++] = (i << kStackBlockBits) | b;
