@@ -73,9 +73,11 @@ def test_stack_k4(cuda, batch):
     assert stack.error() == 0
 
 
-def test_stack_graph_replay_with_new_inputs(cuda):
+@pytest.mark.parametrize("ordered", [False, True])
+def test_stack_graph_replay_with_new_inputs(cuda, ordered):
+    """Every replay rotates the new inputs before any z is read."""
     payloads, stack = _build(cuda, [(d, n, ph) for (d, n), ph in
-                                    zip(QWEN3_4B_LAYER.values(), (0, 0, 0, 1, 2, 2, 3))], 1, ordered=True)
+                                    zip(QWEN3_4B_LAYER.values(), (0, 0, 0, 1, 2, 2, 3))], 1, ordered=ordered)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -91,6 +93,25 @@ def test_stack_graph_replay_with_new_inputs(cuda):
         g.replay()
         torch.cuda.synchronize()
         _check(payloads, stack)
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_stack_split_launches_match_run(cuda, batch):
+    """The two launches called one by one (rotate(), gemv()) give run()'s
+    outputs bit for bit (full-K blocks are deterministic)."""
+    payloads, stack = _build(cuda, MIXED, batch, bias=True)
+    stack.run()
+    torch.cuda.synchronize()
+    fused = [o.clone() for o in stack.outputs]
+    for o in stack.outputs:
+        o.zero_()
+    stack.rotate()
+    stack.gemv()
+    torch.cuda.synchronize()
+    for a, b in zip(fused, stack.outputs):
+        assert torch.equal(a, b)
+    _check(payloads, stack)
+    assert stack.error() == 0
 
 
 def test_stack_rejects_mixed_codebooks(cuda):
