@@ -32,6 +32,10 @@ compute, i.e. the practical ceiling the kernel is compared against.
 skinny GEMM of BASELINE.json configs[4]: the same stack at batch 32 and the
 gate / down shapes per linear at batch 32, as time, TFLOP/s and fraction of
 the 2.5 PFLOP/s dense fp16 MFMA peak.
+``--per-linear`` runs only the one-linear-at-a-time sweep of configs[3] /
+configs[4] (PackedTCQLinear.forward per call, each case cycling over >= 320
+MB of distinct copies) beside the time one streaming-read launch of the same
+byte count takes.
 ``encoder`` (comparison runs only) times the compress-time TCQ Viterbi
 search on a gate_proj-sized matrix; its CPU comparison sits in the
 CPU-baseline leg.
@@ -282,6 +286,72 @@ def batch32_reference(layers, steps: int, warmup: int) -> dict:
     return out
 
 
+def _graph_us_per_call(step_fn, calls: int, steps: int = 20) -> float:
+    """µs per call of a graph of `calls` back-to-back calls (step_fn makes
+    them), replayed `steps` times after 5 warm-up replays."""
+    ms, _, _ = time_graph(step_fn, steps, 5)
+    return ms * 1e3 / calls
+
+
+def per_linear_sweep(cases=None, min_bytes: float = 320e6) -> list:
+    """BASELINE.json configs[3] / configs[4] one linear at a time:
+    PackedTCQLinear.forward (one launch per call) for gate_proj / up_proj /
+    down_proj of Qwen3-4B at k in {2, 3, 4}, B in {1, 4, 8}, plus gate / down
+    at k=3, B=32.  Each case builds R >= min_bytes / bytes distinct device
+    copies of one seeded linear and times one graph of R forwards (so no call
+    reads cached weights).  `floor_us` is the same byte count read by one
+    plain streaming-read launch (tp_read_probe) per call, R distinct buffers
+    in one graph: what a single launch of that size reaches at all."""
+    from turbopress_amd import _lib
+    from turbopress_amd.runtime import PackedTCQLinear
+    from turbopress_amd.synthetic import QWEN3_4B_LAYER, make_activation, make_payload, payload_to
+    if cases is None:
+        cases = [(nm, k, b) for k in (2, 3, 4) for b in (1, 4, 8) for nm in ("gate_proj", "up_proj", "down_proj")]
+        cases += [("gate_proj", 3, 32), ("down_proj", 3, 32)]
+    lib = _lib.lib()
+    floors = {}
+    out = []
+    for name, k, b in cases:
+        d, n = QWEN3_4B_LAYER[name]
+        nb = _bytes(n, d, k, b)
+        reps = max(8, -(-int(min_bytes) // nb))
+        p = payload_to(make_payload(n, d, k, N_STATES, seed=k), "cuda")
+        mods = [PackedTCQLinear(p, mode="hip") for _ in range(reps)]
+        x = make_activation(b, d, seed=1).cuda()
+
+        def step(mods=mods, x=x):
+            for m in mods:
+                m(x)
+
+        us = _graph_us_per_call(step, reps)
+        del mods
+        key = (nb + 15) & ~15
+        if key not in floors:
+            bufs = [torch.ones(key // 4, dtype=torch.int32, device="cuda") for _ in range(reps)]
+            sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+
+            def probe(bufs=bufs, sink=sink, key=key):
+                st = torch.cuda.current_stream().cuda_stream
+                for buf in bufs:
+                    _lib.check(lib.tp_read_probe(buf.data_ptr(), key, sink.data_ptr(), st), "read_probe")
+
+            floors[key] = _graph_us_per_call(probe, reps)
+            del bufs
+        torch.cuda.empty_cache()
+        row = {"linear": name, "bits": k, "batch": b, "us": round(us, 2), "bytes": nb,
+               "gbps": round(nb / (us * 1e-6) / 1e9, 1), "pct_hbm_peak": round(100 * nb / (us * 1e-6) / 1e9
+                                                                                 / HBM_PEAK_GBPS, 2),
+               "floor_us": round(floors[key], 2)}
+        if b >= 16:
+            tfl = 2 * b * n * d / (us * 1e-6) / 1e12
+            row["tflops"] = round(tfl, 2)
+            row["mfma_frac"] = round(tfl / MFMA_FP16_PEAK_TFLOPS, 4)
+        print(f"[bench] {name} k={k} B={b}: {row['us']} us, {row['gbps']} GB/s "
+              f"(one read launch of the same bytes: {row['floor_us']} us)", file=sys.stderr, flush=True)
+        out.append(row)
+    return out
+
+
 def cpu_baseline(budget_s: float):
     """The reference's CPU tiled path (oracle restatement), one Qwen3-4B layer
     at k=3, B=1, repeated until ~budget_s of CPU work, scaled to 36 layers."""
@@ -329,6 +399,10 @@ def main() -> int:
     ap.add_argument("--only-primary", action="store_true", help="skip the comparison executors")
     ap.add_argument("--only-batch32", action="store_true",
                     help="run only the batch-32 leg (profiling the MFMA path) and print its figures")
+    ap.add_argument("--per-linear", action="store_true",
+                    help="run only the one-linear-at-a-time sweep (configs c3 / c4) and print its table")
+    ap.add_argument("--cases", default=None,
+                    help="with --per-linear: comma-separated name:bits:batch cases (default: all of c3 and c4)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: the packed-TCQ decode path is built and measured "
@@ -340,6 +414,12 @@ def main() -> int:
     torch.manual_seed(0)
     dev = torch.device("cuda", 0)
     log = lambda m: print(f"[bench] {m}", file=sys.stderr, flush=True)  # noqa: E731
+    if args.per_linear:
+        cases = None
+        if args.cases:
+            cases = [(c.split(":")[0], int(c.split(":")[1]), int(c.split(":")[2])) for c in args.cases.split(",")]
+        print(json.dumps({"per_linear": per_linear_sweep(cases)}), flush=True)
+        return 0
     log(f"building {N_LAYERS}x7 packed linears (k={BITS}, S={N_STATES}, batch {BATCH})")
     layers, inputs = build_layers(dev)
     nbytes = step_bytes(layers)
