@@ -420,7 +420,7 @@ __device__ __forceinline__ UnitRegs<MW, NZ> stream_load(const SlotEnv& E, const 
   constexpr uint32_t unit_m = 4u * kTileRows * MW * 4u;   // member bytes per unit
   constexpr uint32_t unit_z = kChunkCols * 2u;            // z bytes per unit and batch row
   UnitRegs<MW, NZ> g;
-  g.X = __builtin_amdgcn_raw_buffer_load_b64(c.prs, E.pv, (uint32_t)gu * unit_p, 0);
+  g.X = __builtin_amdgcn_raw_buffer_load_b64(c.prs, E.pv, (uint32_t)gu * unit_p, kWeightPolicy);
   g.M = MemberBuf<MW>::load(c.mrs, E.mv, (uint32_t)gu * unit_m);
   // (uniform by construction; readfirstlane keeps it in a scalar register
   // when the compiler merges it with per-lane values)
