@@ -692,9 +692,9 @@ __device__ __forceinline__ ChunkRegs<MW> load_chunk(const LinearDesc& L, const u
 #pragma unroll
   for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
     const int g = 4 * (gu0 + (u < ngu ? u : 0)) + q;
-    c.X[u] = gld2(pt + (g * kTileRows + r) * 2);
+    c.X[u] = gld2_stream(pt + (g * kTileRows + r) * 2);
 #pragma unroll
-    for (int i = 0; i < MW; ++i) c.M[u][i] = gld(mt + (g * kTileRows + r) * MW + i);
+    for (int i = 0; i < MW; ++i) c.M[u][i] = gld_stream(mt + (g * kTileRows + r) * MW + i);
   }
   return c;
 }

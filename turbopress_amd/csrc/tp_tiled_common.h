@@ -31,6 +31,15 @@ __device__ __forceinline__ uint2 gld2(const void* p) {
 }
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+// Streaming (non-temporal) loads of weight words, which a launch reads once:
+// they leave the caches to the data that waves re-read.
+__device__ __forceinline__ uint32_t gld_stream(const uint32_t* p) {
+  return __builtin_nontemporal_load((const TP_GLOBAL uint32_t*)p);
+}
+__device__ __forceinline__ uint2 gld2_stream(const uint32_t* p) {
+  const u32x2_t v = __builtin_nontemporal_load((const TP_GLOBAL u32x2_t*)p);
+  return uint2{v.x, v.y};
+}
 
 constexpr int kTileRows = 16;
 constexpr int kSegCols = 64;
