@@ -345,7 +345,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     for (int u = 0; u < kLinMaxUnits; ++u) {
       const bool ok = active && u < nu;
       const uint32_t gu = (uint32_t)(ok ? u0 + u : 0);
-      R[u].X = __builtin_amdgcn_raw_buffer_load_b64(prs, ok ? pv : kOutOfRange, gu * unit_p, kWeightPolicy);
+      R[u].X = __builtin_amdgcn_raw_buffer_load_b64(prs, ok ? pv : kOutOfRange, gu * unit_p, weight_policy(MW));
       R[u].M = MemberBuf<MW>::load(mrs, ok ? mv : kOutOfRange, gu * unit_m);
     }
     const uint32_t x1_prev = __builtin_amdgcn_raw_buffer_load_b32(

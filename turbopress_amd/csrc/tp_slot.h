@@ -8,12 +8,14 @@ namespace tp {
 
 constexpr int kBufferFlags = 0x00020000;  // raw buffer, 32-bit data format
 constexpr uint32_t kOutOfRange = 0x80000000u;
-// Cache policy of the weight streams (path / member words), which a launch
-// reads exactly once: sc0 | nt, streaming loads that leave the caches to the
-// data every wave re-reads (z, row scales, descriptors).  On the Qwen3-4B
-// decode-step stack: 256 us per GEMV launch against 263 us with the default
-// policy (interleaved runs, same box).
-constexpr int kWeightPolicy = 3;
+// Cache policy of the weight streams (path / member words, MW member words
+// per lane and unit), which a launch reads exactly once.  At 2-3 bits per
+// weight: sc0 | nt, streaming loads that leave the caches to the data every
+// wave re-reads (z, row scales, descriptors); on the Qwen3-4B decode-step
+// stack 256.4 us per GEMV launch against 263.5 us with the default policy
+// (k=3), 239.2 against 244.2 us (k=2).  At 4 bits (MW = 6), where the
+// stack is HBM-bound, the default policy: 332.5 us against 338.0 us.
+constexpr int weight_policy(int MW) { return MW <= 4 ? 3 : 0; }
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferFlags);
@@ -23,13 +25,13 @@ template <int MW> struct MemberBuf;
 template <> struct MemberBuf<2> {
   typedef u32x2_t type;
   static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
-    return __builtin_amdgcn_raw_buffer_load_b64(r, v, s, kWeightPolicy);
+    return __builtin_amdgcn_raw_buffer_load_b64(r, v, s, weight_policy(2));
   }
 };
 template <> struct MemberBuf<4> {
   typedef u32x4_t type;
   static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, v, s, kWeightPolicy);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, v, s, weight_policy(4));
   }
 };
 // k=4: six words (the k=3 words, then one high-member word per path word)
@@ -42,8 +44,8 @@ template <> struct MemberBuf<6> {
   typedef MemberWords6 type;
   static __device__ __forceinline__ type load(__amdgpu_buffer_rsrc_t r, uint32_t v, uint32_t s) {
     MemberWords6 m;
-    m.lo = __builtin_amdgcn_raw_buffer_load_b128(r, v, s, kWeightPolicy);
-    m.hi = __builtin_amdgcn_raw_buffer_load_b64(r, v + 16u, s, kWeightPolicy);
+    m.lo = __builtin_amdgcn_raw_buffer_load_b128(r, v, s, weight_policy(6));
+    m.hi = __builtin_amdgcn_raw_buffer_load_b64(r, v + 16u, s, weight_policy(6));
     return m;
   }
 };

@@ -420,7 +420,7 @@ __device__ __forceinline__ UnitRegs<MW, NZ> stream_load(const SlotEnv& E, const 
   constexpr uint32_t unit_m = 4u * kTileRows * MW * 4u;   // member bytes per unit
   constexpr uint32_t unit_z = kChunkCols * 2u;            // z bytes per unit and batch row
   UnitRegs<MW, NZ> g;
-  g.X = __builtin_amdgcn_raw_buffer_load_b64(c.prs, E.pv, (uint32_t)gu * unit_p, kWeightPolicy);
+  g.X = __builtin_amdgcn_raw_buffer_load_b64(c.prs, E.pv, (uint32_t)gu * unit_p, weight_policy(MW));
   g.M = MemberBuf<MW>::load(c.mrs, E.mv, (uint32_t)gu * unit_m);
   // (uniform by construction; readfirstlane keeps it in a scalar register
   // when the compiler merges it with per-lane values)
@@ -692,9 +692,9 @@ __device__ __forceinline__ ChunkRegs<MW> load_chunk(const LinearDesc& L, const u
 #pragma unroll
   for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
     const int g = 4 * (gu0 + (u < ngu ? u : 0)) + q;
-    c.X[u] = gld2_stream(pt + (g * kTileRows + r) * 2);
+    c.X[u] = gld2_w<MW>(pt + (g * kTileRows + r) * 2);
 #pragma unroll
-    for (int i = 0; i < MW; ++i) c.M[u][i] = gld_stream(mt + (g * kTileRows + r) * MW + i);
+    for (int i = 0; i < MW; ++i) c.M[u][i] = gld_w<MW>(mt + (g * kTileRows + r) * MW + i);
   }
   return c;
 }

@@ -100,14 +100,14 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
       for (int i = 0; i < MW; ++i) Mw[u][i] = 0;
     }
     if (active) {
-      if (gu0 > 0) x1_last = gld_stream(pt + ((4 * gu0 - 1) * kTileRows + r) * 2 + 1);
+      if (gu0 > 0) x1_last = gld_w<MW>(pt + ((4 * gu0 - 1) * kTileRows + r) * 2 + 1);
 #pragma unroll
       for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
         if (u < ngu) {
           const int g = 4 * (gu0 + u) + q;
-          X[u] = gld2_stream(pt + (g * kTileRows + r) * 2);
+          X[u] = gld2_w<MW>(pt + (g * kTileRows + r) * 2);
 #pragma unroll
-          for (int i = 0; i < MW; ++i) Mw[u][i] = gld_stream(mt + (g * kTileRows + r) * MW + i);
+          for (int i = 0; i < MW; ++i) Mw[u][i] = gld_w<MW>(mt + (g * kTileRows + r) * MW + i);
         }
       }
     }

@@ -31,13 +31,20 @@ __device__ __forceinline__ uint2 gld2(const void* p) {
 }
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-// Streaming (non-temporal) loads of weight words, which a launch reads once:
-// they leave the caches to the data that waves re-read.
-__device__ __forceinline__ uint32_t gld_stream(const uint32_t* p) {
-  return __builtin_nontemporal_load((const TP_GLOBAL uint32_t*)p);
+// Loads of weight words, which a launch reads once (MW member words per lane
+// and unit): streaming (non-temporal) at 2-3 bits per weight, which leaves
+// the caches to the data that waves re-read; plain at 4 bits (MW = 6), where
+// the decode-step stack is HBM-bound and streaming loads measured slower.
+template <int MW>
+__device__ __forceinline__ uint32_t gld_w(const uint32_t* p) {
+  if constexpr (MW <= 4) return __builtin_nontemporal_load((const TP_GLOBAL uint32_t*)p);
+  else return *(const TP_GLOBAL uint32_t*)p;
 }
-__device__ __forceinline__ uint2 gld2_stream(const uint32_t* p) {
-  const u32x2_t v = __builtin_nontemporal_load((const TP_GLOBAL u32x2_t*)p);
+template <int MW>
+__device__ __forceinline__ uint2 gld2_w(const uint32_t* p) {
+  u32x2_t v;
+  if constexpr (MW <= 4) v = __builtin_nontemporal_load((const TP_GLOBAL u32x2_t*)p);
+  else v = *(const TP_GLOBAL u32x2_t*)p;
   return uint2{v.x, v.y};
 }
 
