@@ -314,7 +314,12 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   const uint32_t tile_m = (uint32_t)a.G4 * unit_m;  // member bytes of one tile
   int staged = -1;
 
-  for (int g = blockIdx.x; g < a.groups; g += gridDim.x) {
+  // One tile group.  The first call (the workgroup's own group; the host
+  // gives every workgroup one group when they fit) is a copy of its own, so
+  // that its loads are scheduled from the kernel's entry state rather than
+  // from the merged state of a loop: at the loop head the wait before the
+  // weight loads also covered the activation prefetch.
+  auto group = [&](const int g) __attribute__((always_inline)) {
     int p = 0;
     LinPart P = a.part[0];
     if constexpr (MULTI) {
@@ -413,7 +418,9 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
         }
       }
     }
-  }
+  };
+  group((int)blockIdx.x);
+  for (int g = (int)(blockIdx.x + gridDim.x); g < a.groups; g += (int)gridDim.x) group(g);
 }
 
 // ---------------------------------------------------------------------------
