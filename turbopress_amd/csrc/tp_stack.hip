@@ -762,9 +762,12 @@ __device__ __forceinline__ void wide_unit(const uint2 X, const uint32_t* Mw, con
 // adds its sums into the linear's workspace with device-scope atomics, and
 // the wave that completes a tile's K range (counted per tile) writes y and
 // clears the sums (the split-K protocol of tcq_gemv_tiled_kernel).
+// build_table: the pair table is built here (from cb_lane), after the first
+// chunk's z and weight loads are issued, so that neither waits for it.
 template <int KB, int NS, int NBT>
 __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const uint16_t* z, int zld, int batch,
-                           uint16_t* zl, const uint32_t* table, uint32_t laneoff, int tid, int wave, int lane) {
+                           uint16_t* zl, uint32_t* table, uint32_t laneoff, int tid, int wave, int lane,
+                           bool build_table = false, uint32_t cb_lane = 0) {
   constexpr int MW = member_words(KB);
   const int r = lane & 15, q = lane >> 4;
   const int t = wb * kWideWaves + wave;
@@ -779,10 +782,13 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
   for (int bt = 0; bt < NBT; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
   // halo of the range's first unit: word 1 of the previous unit's last segment
   uint32_t x1_last = ch0 > 0 ? pt[((4 * ch0 * kMaxUnitsPerBlock - 1) * kTileRows + r) * 2 + 1] : 0u;
-  {
-    const ZChunk c0 = wide_load_z(zrs, zld, batch, ch0, tid);
-    wide_store_z(zl + (ch0 & 1) * kWideChunkHalves, c0, batch, tid);
-  }
+  // The first chunk's z, then its weights: the z staging waits for the z
+  // loads only, and the weights are in flight during it (and during the
+  // table build).
+  const ZChunk c0 = wide_load_z(zrs, zld, batch, ch0, tid);
+  ChunkRegs<MW> ra = load_chunk<MW>(L, pt, mt, ch0, q, r);
+  if (build_table) build_pair_table_lanes<KB>(table, cb_lane, tid, kWideThreads);
+  wide_store_z(zl + (ch0 & 1) * kWideChunkHalves, c0, batch, tid);
   __syncthreads();
   // Chunk ch: prefetch chunk ch + 1 of z, decode + multiply ch, store the
   // prefetch into the other buffer, one barrier (the next chunk's buffer is
@@ -808,7 +814,6 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
     if (more) wide_store_z(zl + ((ch + 1) & 1) * kWideChunkHalves, nx, batch, tid);
     __syncthreads();
   };
-  ChunkRegs<MW> ra = load_chunk<MW>(L, pt, mt, ch0, q, r);
   for (int ch = ch0; ch < ch1; ch += 2) {
     const ChunkRegs<MW> rb = load_chunk<MW>(L, pt, mt, ch + 1 < ch1 ? ch + 1 : ch, q, r);
     body(ch, ra);
@@ -943,13 +948,12 @@ tcq_wide_linear_kernel(const LinearDesc L, const uint16_t* __restrict__ z, int z
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t laneoff = lane_offsets<KB>(lane);
   const uint32_t cb_lane = gld(codebook + (lane & ((2 << KB) - 1)));
-  build_pair_table_lanes<KB>(table, cb_lane, tid, kWideThreads);
-  __syncthreads();
-  // workgroup (x, y) = (wide block, K part of cps chunks)
+  // workgroup (x, y) = (wide block, K part of cps chunks); the table is
+  // built inside, once the first loads are in flight
   const int nch = (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock;
   const int ch0 = (int)blockIdx.y * cps;
   wide_block<KB, NS, NBT>(L, (int)blockIdx.x, ch0, min(nch, ch0 + cps), z, zld, batch, zl, table, laneoff, tid,
-                          wave, lane);
+                          wave, lane, true, cb_lane);
 }
 
 template <int KB, int NS>

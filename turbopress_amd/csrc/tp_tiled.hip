@@ -66,7 +66,11 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
   bool table_ready = false;
   const uint32_t cb_lane = a.codebook[lane & ((2 << KB) - 1)];
 
-  for (int blk = blockIdx.x; blk < a.total_blocks; blk += gridDim.x) {
+  // One block.  The first call (the workgroup's first block) is a copy of
+  // its own, so that its loads are scheduled from the kernel's entry state
+  // rather than from the merged state of a loop: at the loop head the weight
+  // loads waited for every earlier load, the codebook load included.
+  auto block = [&](const int blk) __attribute__((always_inline)) {
     int li = 0, base = 0;
 #pragma unroll
     for (int i = 0; i < kMaxInlineLinears - 1; ++i) {
@@ -125,7 +129,7 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
       stage_z<ROT>(L, gu0, ngu, batch, zl, wave, lane);
     }
     __syncthreads();
-    if (!active) continue;
+    if (!active) return;
 
     float4_t acc[NBT];
 #pragma unroll
@@ -206,7 +210,9 @@ tcq_gemv_tiled_kernel(const GemvArgs a) {
         if (lane == 0) atomicExch(L.cnt + t, 0u);
       }
     }
-  }
+  };
+  block((int)blockIdx.x);
+  for (int blk = (int)(blockIdx.x + gridDim.x); blk < a.total_blocks; blk += (int)gridDim.x) block(blk);
 }
 
 // ---------------------------------------------------------------------------
