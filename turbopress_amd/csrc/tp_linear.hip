@@ -460,10 +460,11 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   const int64_t G4 = g0.G4;
   if (G4 > (int64_t)kLinWaves * kLinMaxUnits) return kLinearNotHandled;
   if (rot && hb > 2 * kChunkCols && G4 * kChunkCols != d) return kLinearNotHandled;
-  // Staging issues the activations of two items per wave ahead of the
-  // weights; each further item costs a dependent round trip, so larger
-  // inputs (batch * 256-column chunks) keep the split-K kernel.
-  if (batch * G4 > (int64_t)kLinWaves * (lin_pre(bits) + 1) || batch > 4) return kLinearNotHandled;
+  // Staging issues the activations of lin_pre(bits) items per wave ahead
+  // of the weights; each further item costs a dependent round trip, so
+  // inputs of more than 3 items per wave (batch * 256-column chunks) keep
+  // the split-K kernel.
+  if (batch * G4 > (int64_t)kLinWaves * (kLinPre + 1) || batch > 4) return kLinearNotHandled;
 
   // LDS: 64 KiB table (static) + z rows + max(partial sums, one fp32 row).
   const int64_t zstride = G4 * kChunkCols + 8;
