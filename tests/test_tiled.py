@@ -173,10 +173,12 @@ FUSED_CASES = [  # (n, d, bits): Hadamard block d & -d = 2, 4, 64, 512, 1024, 20
 
 
 @pytest.mark.parametrize("n,d,bits", FUSED_CASES)
-@pytest.mark.parametrize("batch", [1, 4, 20])
+@pytest.mark.parametrize("batch", [1, 4, 12, 20])
 def test_fused_forward_matches_oracle(cuda, n, d, bits, batch):
     """tp_packed_linear_forward: rotation computed per workgroup in LDS (full
-    blocks, partial blocks of a larger Hadamard, unaligned d fallback)."""
+    blocks, partial blocks of a larger Hadamard, unaligned d fallback); at
+    batch 12 / 20 with blocks <= 512 the wide kernel rotates each 512-column
+    chunk itself (one and two 16-row batch tiles)."""
     from turbopress_amd.runtime import PackedTCQLinear
     p = make_payload(n, d, bits, 64, seed=d + batch, bias=True)
     lin = PackedTCQLinear(p, mode="hip")
@@ -193,6 +195,21 @@ def test_fused_equals_two_launch_path(cuda):
     x = make_activation(3, 9728, seed=9).to(cuda)
     fused = lin(x).float()
     two = hk.packed_gemv(hk.fwht_scale(x, lin.rot_scale, lin.block), lin).float()
+    assert float((fused - two).abs().max()) <= 2e-3 * float(two.abs().max())
+
+
+@pytest.mark.parametrize("batch", [12, 32])
+def test_fused_wide_equals_two_launch_path(cuda, batch):
+    """Batch 9..32 at Hadamard block 512: the wide kernel rotating in the
+    launch matches the rotation launch + wide kernel on z."""
+    from turbopress_amd import hip_kernel as hk
+    from turbopress_amd.runtime import PackedTCQLinear
+    p = make_payload(9728, 2560, 3, 64, seed=11)
+    lin = PackedTCQLinear(p, mode="hip")
+    x = make_activation(batch, 2560, seed=12).to(cuda)
+    fused = lin(x).float()
+    zpad = hk.rotate_padded(x, lin.rot_scale, lin.block, lin._tiled_geo["z_cols"])
+    two = hk.gemv_tiled(zpad, lin, lin.bias, torch.empty(batch, 9728, dtype=torch.float16, device=cuda)).float()
     assert float((fused - two).abs().max()) <= 2e-3 * float(two.abs().max())
 
 

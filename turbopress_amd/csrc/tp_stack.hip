@@ -726,6 +726,73 @@ __device__ __forceinline__ void wide_store_z(uint16_t* zb, const ZChunk& c, int 
   }
 }
 
+// ROT (per-linear launches at Hadamard blocks <= 512, every chunk then a
+// whole number of blocks): thread tid's two 8-column pieces of chunk ch of
+// the unrotated input and of rot_scale (columns past d read as zero).
+struct XChunk {
+  u32x4_t x[2], r[2];
+};
+__device__ __forceinline__ XChunk wide_load_x(const LinearDesc& L, int batch, int ch, int tid) {
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(L.x, (uint32_t)(batch * L.ldx) * 2u);
+  const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(L.rs, (uint32_t)L.d * 2u);
+  XChunk c;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int i = tid + kWideThreads * k;
+    const int row = i >> 6, col = ch * kZCols + (i & 63) * 8;
+    const bool in = row < batch && col < L.d;  // d % 8 == 0: a piece is wholly in or out
+    c.x[k] = __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? (uint32_t)(row * L.ldx + col) * 2u : kOutOfRange, 0, 0);
+    c.r[k] = __builtin_amdgcn_raw_buffer_load_b128(rrs, in ? (uint32_t)col * 2u : kOutOfRange, 0, 0);
+  }
+  return c;
+}
+
+// z = fp16(blockFWHT(x * rot_scale) / sqrt(hb)) of the pieces: a wave holds
+// one row's 512 columns (8 per lane), so the butterflies at distance 1..4
+// run in registers and 8..256 across lanes, in increasing distance as the
+// reference's transform, all in fp32, one rounding to fp16.
+__device__ __forceinline__ ZChunk wide_rotate(const XChunk& c, int lane, int hb, float hdiv) {
+  ZChunk z;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t xw = c.x[k][e], rw = c.r[k][e];
+      v[2 * e] = h2f((uint16_t)xw) * h2f((uint16_t)rw);
+      v[2 * e + 1] = h2f((uint16_t)(xw >> 16)) * h2f((uint16_t)(rw >> 16));
+    }
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1) {
+      if (h < hb) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if ((e & h) == 0) {
+            const float a = v[e], b = v[e + h];
+            v[e] = a + b;
+            v[e + h] = a - b;
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int sft = 0; sft < 6; ++sft) {
+      if ((8 << sft) < hb) {
+        const bool upper = (lane >> sft) & 1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float p = __shfl_xor(v[e], 1 << sft, 64);
+          v[e] = upper ? p - v[e] : v[e] + p;
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      z.v[k][e] = (uint32_t)f2h(v[2 * e] / hdiv) | ((uint32_t)f2h(v[2 * e + 1] / hdiv) << 16);
+  }
+  return z;
+}
+
 // One unit of one wave of the wide kernel: decode 64 weights per lane, then
 // for each of the 8 MFMA positions read the B operands of the NBT batch tiles
 // from the staged chunk (rows past the batch hold stale data: their MFMA
@@ -764,7 +831,8 @@ __device__ __forceinline__ void wide_unit(const uint2 X, const uint32_t* Mw, con
 // clears the sums (the split-K protocol of tcq_gemv_tiled_kernel).
 // build_table: the pair table is built here (from cb_lane), after the first
 // chunk's z and weight loads are issued, so that neither waits for it.
-template <int KB, int NS, int NBT>
+// ROT: z is computed from L.x and L.rs chunk by chunk (wide_rotate).
+template <int KB, int NS, int NBT, bool ROT = false>
 __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const uint16_t* z, int zld, int batch,
                            uint16_t* zl, uint32_t* table, uint32_t laneoff, int tid, int wave, int lane,
                            bool build_table = false, uint32_t cb_lane = 0) {
@@ -785,9 +853,13 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
   // The first chunk's z, then its weights: the z staging waits for the z
   // loads only, and the weights are in flight during it (and during the
   // table build).
-  const ZChunk c0 = wide_load_z(zrs, zld, batch, ch0, tid);
+  ZChunk c0;
+  XChunk x0;
+  if constexpr (ROT) x0 = wide_load_x(L, batch, ch0, tid);
+  else c0 = wide_load_z(zrs, zld, batch, ch0, tid);
   ChunkRegs<MW> ra = load_chunk<MW>(L, pt, mt, ch0, q, r);
   if (build_table) build_pair_table_lanes<KB>(table, cb_lane, tid, kWideThreads);
+  if constexpr (ROT) c0 = wide_rotate(x0, lane, L.hb, L.hdiv);
   wide_store_z(zl + (ch0 & 1) * kWideChunkHalves, c0, batch, tid);
   __syncthreads();
   // Chunk ch: prefetch chunk ch + 1 of z, decode + multiply ch, store the
@@ -796,7 +868,11 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
   auto body = [&](int ch, const ChunkRegs<MW>& regs) {
     const bool more = ch + 1 < ch1;
     ZChunk nx;
-    if (more) nx = wide_load_z(zrs, zld, batch, ch + 1, tid);
+    XChunk nxx;
+    if (more) {
+      if constexpr (ROT) nxx = wide_load_x(L, batch, ch + 1, tid);
+      else nx = wide_load_z(zrs, zld, batch, ch + 1, tid);
+    }
     const uint16_t* zb = zl + (ch & 1) * kWideChunkHalves;
     if (active) {
       const int gu0 = ch * kMaxUnitsPerBlock;
@@ -811,7 +887,10 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
         }
       }
     }
-    if (more) wide_store_z(zl + ((ch + 1) & 1) * kWideChunkHalves, nx, batch, tid);
+    if (more) {
+      if constexpr (ROT) nx = wide_rotate(nxx, lane, L.hb, L.hdiv);
+      wide_store_z(zl + ((ch + 1) & 1) * kWideChunkHalves, nx, batch, tid);
+    }
     __syncthreads();
   };
   for (int ch = ch0; ch < ch1; ch += 2) {
@@ -937,7 +1016,7 @@ tcq_stack_wide_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
 
 // One linear at batch 9..32 with its rotated activations already in z
 // (fp16 [batch][zld], zero past d): one workgroup per wide block.
-template <int KB, int NS, int NBT>
+template <int KB, int NS, int NBT, bool ROT>
 __global__ void __launch_bounds__(kWideThreads)
 tcq_wide_linear_kernel(const LinearDesc L, const uint16_t* __restrict__ z, int zld, int batch,
                        const uint16_t* __restrict__ codebook, int cps) {
@@ -952,8 +1031,8 @@ tcq_wide_linear_kernel(const LinearDesc L, const uint16_t* __restrict__ z, int z
   // built inside, once the first loads are in flight
   const int nch = (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock;
   const int ch0 = (int)blockIdx.y * cps;
-  wide_block<KB, NS, NBT>(L, (int)blockIdx.x, ch0, min(nch, ch0 + cps), z, zld, batch, zl, table, laneoff, tid,
-                          wave, lane, true, cb_lane);
+  wide_block<KB, NS, NBT, ROT>(L, (int)blockIdx.x, ch0, min(nch, ch0 + cps), z, zld, batch, zl, table, laneoff,
+                               tid, wave, lane, true, cb_lane);
 }
 
 template <int KB, int NS>
@@ -968,7 +1047,8 @@ void launch_wide_linear(const LinearDesc& L, const uint16_t* z, int zld, int bat
   const int cps = (nch + parts - 1) / parts;
   const dim3 grid(groups, (nch + cps - 1) / cps);
   const size_t zbytes = (size_t)2 * kWideChunkHalves * 2;
-  auto kern = batch <= 16 ? tcq_wide_linear_kernel<KB, NS, 1> : tcq_wide_linear_kernel<KB, NS, 2>;
+  auto kern = z ? (batch <= 16 ? tcq_wide_linear_kernel<KB, NS, 1, false> : tcq_wide_linear_kernel<KB, NS, 2, false>)
+               : (batch <= 16 ? tcq_wide_linear_kernel<KB, NS, 1, true> : tcq_wide_linear_kernel<KB, NS, 2, true>);
   allow_dynamic_lds(reinterpret_cast<const void*>(kern), kTableBytes + 256);
   hipLaunchKernelGGL(kern, grid, dim3(kWideThreads), zbytes, s, L, z, zld, batch, cb, cps);
 }
@@ -977,6 +1057,10 @@ int linear_forward_wide(const LinearDesc& Lin, const uint16_t* z, int64_t zld, i
                         const uint16_t* codebook, int bits, int n_states, void* workspace, int64_t workspace_bytes,
                         hipStream_t s) {
   if (batch <= 8 || batch > 32) return kLinearNotHandled;
+  // z null: rotate L.x * L.rs chunk by chunk in the launch (each 512-column
+  // chunk a whole number of Hadamard blocks; 16-byte input pieces)
+  if (!z && (Lin.hb > kZCols || Lin.d % 8 || Lin.ldx % 8 || ((uintptr_t)Lin.x & 15) || ((uintptr_t)Lin.rs & 15)))
+    return kLinearNotHandled;
   // split-K sums: fp32 [T * 16 rows][16 * NBT] then one counter per tile
   LinearDesc L = Lin;
   const int64_t nbt = batch <= 16 ? 1 : 2;

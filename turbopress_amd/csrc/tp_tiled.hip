@@ -534,14 +534,21 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
   // Batch <= 8 runs the one-pass kernel (tp_linear.hip) when it applies.
   const int fast = linear_forward_fast(ls, n_lin, batch, codebook, bits, n_states, (hipStream_t)stream);
   if (fast != kLinearNotHandled) return fast;
-  // Batch 9..32 on rotated activations: 16-tile blocks through LDS (tp_stack.hip).
-  if (!rot && batch > 8) {
-    for (int i = 0; i < n_lin; ++i) {
-      const int st = linear_forward_wide(a.lin[i], ls[i].x, ls[i].ldx, batch, codebook, bits, n_states,
-                                         ls[i].workspace, ls[i].workspace_bytes, (hipStream_t)stream);
-      if (st) return st;
+  // Batch 9..32: 16-tile blocks through LDS (tp_stack.hip), on rotated
+  // activations or rotating them in the launch (blocks <= 512).
+  if (batch > 8) {
+    bool wide = true;
+    for (int i = 0; i < n_lin && rot; ++i)
+      wide = wide && a.lin[i].hb <= kZCols && a.lin[i].d % 8 == 0 && a.lin[i].ldx % 8 == 0 &&
+             !((uintptr_t)a.lin[i].x & 15) && !((uintptr_t)a.lin[i].rs & 15);
+    if (wide) {
+      for (int i = 0; i < n_lin; ++i) {
+        const int st = linear_forward_wide(a.lin[i], rot ? nullptr : ls[i].x, ls[i].ldx, batch, codebook, bits,
+                                           n_states, ls[i].workspace, ls[i].workspace_bytes, (hipStream_t)stream);
+        if (st) return st;
+      }
+      return TP_OK;
     }
-    return TP_OK;
   }
   a.total_blocks = (int32_t)total_blocks;
   const int wg_per_cu = nbt == 1 ? 2 : 1;

@@ -565,11 +565,12 @@ constexpr int kLinearNotHandled = 1 << 20;
 int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
                         int bits, int n_states, hipStream_t s);
 
-// Batch 9..32 decode-GEMV of one linear whose activations are already
-// rotated (z fp16 [batch][zld], zero past d), in 16-tile blocks, K split
-// across workgroups through the workspace (tp_gemv_workspace_bytes) when one
-// is given (tp_stack.hip).  Returns a status, or kLinearNotHandled for
-// other batches.
+// Batch 9..32 decode-GEMV of one linear, in 16-tile blocks, K split across
+// workgroups through the workspace (tp_gemv_workspace_bytes) when one is
+// given (tp_stack.hip): on rotated activations (z fp16 [batch][zld], zero
+// past d), or with z null on L.x / L.rs, rotated in the launch (Hadamard
+// block <= 512, d and ldx multiples of 8, 16-byte aligned x and rot_scale).
+// Returns a status, or kLinearNotHandled for other batches or layouts.
 int linear_forward_wide(const LinearDesc& L, const uint16_t* z, int64_t zld, int64_t batch,
                         const uint16_t* codebook, int bits, int n_states, void* workspace, int64_t workspace_bytes,
                         hipStream_t s);

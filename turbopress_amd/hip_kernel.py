@@ -216,16 +216,18 @@ def gemv_tiled(zpad: Tensor, layer, bias: Tensor | None, out: Tensor) -> Tensor:
 
 
 def forward_tiled(layer, x: Tensor) -> Tensor:
-    """Rotation + decode-GEMV + bias: one fused launch per call at up to 8
-    rows (tp_packed_linear_forward); more rows rotate once into the padded
-    layout and run the batched decode-GEMV (tp_tcq_gemv_tiled) per 32 rows.
-    fp16 [..., n]."""
+    """Rotation + decode-GEMV + bias: one fused launch per 32 rows
+    (tp_packed_linear_forward) when the rotation fits the launch (up to 8
+    rows, or Hadamard blocks <= 512); otherwise the rows rotate once into the
+    padded layout and run the batched decode-GEMV (tp_tcq_gemv_tiled) per 32
+    rows.  fp16 [..., n]."""
     _require_cuda(x, "x")
     n, d = layer.out_features, layer.in_features
     flat = x.reshape(-1, d).to(torch.float16).contiguous()
     y = torch.empty(flat.shape[0], n, dtype=torch.float16, device=x.device)
-    if d % 4 or flat.shape[0] > 8:
-        # Rows not 8-byte aligned, or a batch: rotate into the padded layout, then GEMV.
+    if d % 4 or (flat.shape[0] > 8 and (layer.block > 512 or d % 8)):
+        # Rows not 8-byte aligned, or a batch whose Hadamard blocks span more
+        # than one 512-column chunk: rotate into the padded layout, then GEMV.
         zpad = rotate_padded(flat, layer.rot_scale, layer.block, layer._tiled_geo["z_cols"])
         gemv_tiled(zpad, layer, layer.bias, y)
         return y.reshape(*x.shape[:-1], n)
