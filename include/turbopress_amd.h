@@ -42,12 +42,6 @@ int tp_abi_version(void);
 /* Static, human-readable name of a status code. */
 const char* tp_status_string(int status);
 
-/* Keep `stream` busy for about `microseconds` (<= 1e6) with a single-wave
- * kernel that polls the GPU wall clock and always terminates.  Benchmark
- * utility: lets a host enqueue timed work ahead of the GPU.  No reference
- * counterpart (the reference times with host clocks, scripts/bench_packed.py). */
-int tp_device_delay(int64_t microseconds, void* stream);
-
 /* Read `bytes` (a multiple of 16, 16-byte aligned) of device memory once
  * with a plain streaming-read kernel (grid-stride 16-byte loads, 4
  * workgroups per CU); `sink` (one device word) is written only in the
@@ -234,7 +228,8 @@ typedef struct tp_stack_linear {
 
 /* Bytes of the device plan of these linears at this batch (0 when invalid):
  * descriptors, schedules, counters and the buffer of rotated activations
- * (batch * ceil(d/256)*256 fp16 per linear).  Host only. */
+ * (batch * ceil(d/256)*256 fp16 per linear).  A plan holds 1..65536
+ * linears of at most 2^21 rows each, in at most 4096 phases.  Host only. */
 int64_t tp_stack_plan_bytes(const tp_stack_linear* linears, int n_linears, int bits, int64_t batch);
 
 /* Validate the linears and write the plan (descriptors, block prefix sums,

@@ -75,6 +75,29 @@ def test_host_side_argument_validation(built_lib):
     assert built_lib.tp_read_probe(ctypes.c_void_p(24), 64, fake, None) == _lib.TP_ERR_MISALIGNED
 
 
+def _stack_array(count, n=256, d=256):
+    from turbopress_amd import _lib
+    arr = (_lib.StackLinear * count)()
+    for i in range(count):
+        arr[i].n, arr[i].d, arr[i].ldx, arr[i].ldy, arr[i].block, arr[i].phase = n, d, d, n, d & -d, 0
+    return arr
+
+
+def test_stack_plan_size_limits(built_lib):
+    """Schedule entries hold (linear << 14) | block in a positive int32: the
+    plan accepts up to 65536 linears of up to 2^14 blocks (128 rows each) and
+    refuses anything larger on the host."""
+    assert built_lib.tp_stack_plan_bytes(_stack_array(1), 1, 3, 1) > 0
+    assert built_lib.tp_stack_plan_bytes(_stack_array(2048), 2048, 3, 1) > 0
+    big = _stack_array(65536, n=16, d=64)
+    assert built_lib.tp_stack_plan_bytes(big, 65536, 3, 1) > 0
+    assert built_lib.tp_stack_plan_bytes(_stack_array(65537, n=16, d=64), 65537, 3, 1) == 0
+    assert built_lib.tp_stack_plan_bytes(_stack_array(1, n=128 << 14, d=64), 1, 3, 1) == 0
+    assert built_lib.tp_stack_plan_bytes(_stack_array(1, n=(128 << 14) - 128, d=64), 1, 3, 1) > 0
+    assert built_lib.tp_stack_plan_bytes(_stack_array(1), 1, 5, 1) == 0
+    assert built_lib.tp_stack_plan_bytes(_stack_array(1), 1, 3, 33) == 0
+
+
 def test_check_maps_status_to_reference_exceptions():
     from turbopress_amd import _lib
     with pytest.raises(ValueError):

@@ -56,7 +56,7 @@ def test_fwht_scale_rejects_bad_block(cuda):
 
 # -------------------------------------------------------------------- decode
 DECODE_CASES = [(n, d, k, s) for s in (4, 8, 16, 64) for (n, d, k) in
-                ((5, 78, 1), (9, 96, 2), (7, 102, 3), (3, 130, 4), (4, 64, 5), (2, 40, 7))]
+                ((5, 77, 1), (9, 96, 2), (7, 102, 3), (3, 130, 4), (4, 64, 5), (2, 40, 7))]
 
 
 @pytest.mark.parametrize("n,d,bits,n_states", DECODE_CASES)
@@ -143,6 +143,28 @@ def test_forward_errors_match_reference(cuda):
         PackedTCQLinear(p, mode="warp")
     with pytest.raises(ValueError):
         PackedTCQLinear({"format": 1})
+
+
+@pytest.mark.parametrize("n,d,bits", [(9728, 2560, 3), (2560, 9728, 2), (100, 300, 4)])
+def test_packed_bytes_exact(cuda, n, d, bits):
+    """packed_bytes follows the reference's accounting (runtime.py:337-356)
+    with the device layout in place of the (k+1)-bit level stream: exactly
+    k bits per weight of the padded 16-row x 256-column tiles, plus the fp16
+    side tensors; cached mode counts the fp16 weights."""
+    from turbopress_amd.runtime import PackedTCQLinear
+    p = make_payload(n, d, bits, 64, seed=5, bias=True)
+    n_pad, d_pad = -(-n // 16) * 16, -(-d // 256) * 256
+    side = 2 * (n + (1 << (bits + 1))) + 2 * n  # scales, codebook, bias
+    signs = (d + 7) // 8
+    hip = PackedTCQLinear(p, mode="hip")
+    assert hip.tiled_packed.numel() == n_pad * d_pad * bits // 8
+    assert hip.packed_bytes() == n_pad * d_pad * bits // 8 + signs + 2 * (2 * d) + side
+    tiled = PackedTCQLinear(p, mode="tiled")
+    natural = n * ((d + 7) // 8) + n * ((d * (bits - 1) + 7) // 8)
+    assert tiled.packed_bytes() == natural + signs + 2 * (2 * d) + side
+    if n * d <= 1 << 20:
+        cached = PackedTCQLinear(p, mode="cached")
+        assert cached.packed_bytes() == 2 * n * d + side
 
 
 def test_packed_bytes_and_attributes(cuda):

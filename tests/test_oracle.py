@@ -269,6 +269,28 @@ def test_tiled_forward_matches_fp64_dense():
     assert O.max_rel(y, ref) < 1e-3
 
 
+@pytest.mark.parametrize("bits,n_states,batch", [(2, 8, 1), (3, 64, 3), (4, 16, 2)])
+def test_gemv_fp64_matches_independent_dense_product(bits, n_states, batch):
+    """gemv_fp64 (window decode, row scale factored out of the sum) against
+    an independent statement: levels from the sequential shift-register walk
+    (trellis.py:182-199), dense weights cb[level] * scale in fp64, then a
+    plain row-by-row dot product.  A transposed operand, a dropped scale or a
+    reversed window fails it."""
+    p = _payload(n=24, d=80, bits=bits, n_states=n_states, seed=7, bias=False)
+    z = np.random.default_rng(bits).standard_normal((batch, 80))
+    got = O.gemv_fp64(p, z)
+    lv = O.decode_levels_sequential(O.unpack_le(p["path_packed"], 80, 1),
+                                    O.unpack_le(p["member_packed"], 80, bits - 1), n_states)
+    cb = p["codebook"].astype(np.float64)
+    sc = p["scales"].astype(np.float64)
+    ref = np.empty((batch, 24))
+    for b in range(batch):
+        for r in range(24):
+            ref[b, r] = sum(cb[lv[r, c]] * sc[r] * z[b, c] for c in range(80))
+    assert got.shape == (batch, 24)
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
 def test_torch_tiled_baseline_agrees_with_numpy_oracle():
     from oracle.tiled_baseline import TiledLinearCPU
     from turbopress_amd.synthetic import make_payload, payload_numpy

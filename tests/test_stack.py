@@ -124,3 +124,40 @@ def test_stack_rejects_mixed_codebooks(cuda):
         LinearStack([(a, x, 0), (b, x, 0)])
     with pytest.raises(ValueError):
         LinearStack([(a, x, 1), (a, x, 0)])  # phases must not decrease
+
+
+def test_headline_plan_matches_per_linear_and_oracle(cuda):
+    """The exact plan bench.py times: Qwen3-4B, 36 layers x 7 linears (252
+    linears, 144 phases, 1.37 GB), k=3, S=64, batch 1.  Every stack output,
+    unordered and phase-ordered, within max-rel 2e-3 of the per-linear
+    PackedTCQLinear.forward on the same input, and layers 0 and 35 within
+    2e-3 of the oracle's tiled forward."""
+    import bench
+    layers, inputs = bench.build_layers(cuda)
+    payload_of = {}
+    from turbopress_amd.synthetic import QWEN3_4B_LAYER as SH
+    for li in (0, 35):
+        for j, name in enumerate(bench.ORDER):
+            d, n = SH[name]
+            payload_of[(li, name)] = make_payload(n, d, 3, 64, seed=1000 * li + j)
+    refs = [mods[name](xs[bench.GROUP_INPUT[name]]).float()
+            for mods, xs in zip(layers, inputs) for name in bench.ORDER]
+    for ordered in (False, True):
+        stack = bench.make_stack(layers, inputs, ordered=ordered)
+        assert len(stack.linears) == 252 and stack.n_phases == 144
+        for _ in range(2):  # the second run starts from the counters the first one reset
+            for o in stack.outputs:
+                o.fill_(float("nan"))
+            stack.run()
+            torch.cuda.synchronize()
+            for i, (got, ref) in enumerate(zip(stack.outputs, refs)):
+                err = float((got.float() - ref).abs().max() / ref.abs().max())
+                assert err <= GEMV_TOL, (ordered, i // 7, bench.ORDER[i % 7], err)
+        assert stack.error() == 0
+        if not ordered:
+            for (li, name), p in payload_of.items():
+                i = 7 * li + bench.ORDER.index(name)
+                x = inputs[li][bench.GROUP_INPUT[name]].cpu().numpy()
+                ref = O.tiled_forward(payload_numpy(p), x)
+                assert O.max_rel(stack.outputs[i].float().cpu().numpy(), ref) <= GEMV_TOL, (li, name)
+        del stack

@@ -232,3 +232,37 @@ def test_group_forward_matches_oracle(cuda, shapes, batch):
         assert o.shape == (batch, n)
         ref = O.tiled_forward(payload_numpy(p), x.numpy())
         assert O.max_rel(o.float().cpu().numpy(), ref) <= GEMV_TOL
+
+
+@pytest.mark.parametrize("d,block", [(3072, 1024), (4096, 4096), (2560, 512)])
+@pytest.mark.parametrize("batch", [12, 20])
+@pytest.mark.parametrize("x_offset", [0, 8])
+def test_packed_linear_forward_abi_batch_9_to_32(cuda, d, block, batch, x_offset):
+    """tp_packed_linear_forward called through the C ABI at batch 9..32: with a
+    Hadamard block over 512 or an x that is only 8-byte aligned it runs the
+    split-K kernel with the rotation fused per workgroup (the path Python's
+    forward_tiled routes around); with block 512 and 16-byte aligned x the
+    wide kernel rotating each chunk itself."""
+    from turbopress_amd import _lib
+    from turbopress_amd.runtime import PackedTCQLinear
+    n = 200
+    p = make_payload(n, d, 3, 64, seed=d + batch, bias=True)
+    assert p["block"] == block
+    lin = PackedTCQLinear(p, mode="hip")
+    x = make_activation(batch, d, seed=batch + x_offset)
+    # x placed `x_offset` bytes past a 16-byte aligned base
+    raw = torch.zeros(batch * d + 8, dtype=torch.float16, device=cuda)
+    xs = raw[x_offset // 2: x_offset // 2 + batch * d].view(batch, d)
+    xs.copy_(x.to(cuda))
+    assert xs.data_ptr() % 16 == x_offset
+    y = torch.full((batch, n), float("nan"), dtype=torch.float16, device=cuda)
+    buf, pb = lin.tiled_packed, lin._tiled_geo["path_bytes"]
+    st = _lib.lib().tp_packed_linear_forward(
+        xs.data_ptr(), d, batch, lin.rot_scale.data_ptr(), block, buf.data_ptr(), buf.data_ptr() + pb,
+        lin.scales.data_ptr(), lin.codebook.data_ptr(), lin.bias.data_ptr(), n, d, 3, 64, y.data_ptr(), n,
+        lin._gemv_ws.data_ptr(), lin._gemv_ws.numel(), torch.cuda.current_stream(cuda).cuda_stream)
+    assert st == 0
+    torch.cuda.synchronize()
+    ref = O.tiled_forward(payload_numpy(p), x.numpy())
+    assert O.max_rel(y.float().cpu().numpy(), ref) <= GEMV_TOL
+    assert int(lin._gemv_ws.count_nonzero()) == 0  # split-K workspace back to zero

@@ -32,7 +32,6 @@ SIGNATURES: dict[str, tuple] = {
     "tp_abi_version": (c_int, []),
     "tp_status_string": (c_char_p, [c_int]),
     "tp_subset_lut": (c_int, [c_int, POINTER(c_uint8), c_int]),
-    "tp_device_delay": (c_int, [_I64, _P]),
     "tp_read_probe": (c_int, [_P, _I64, _P, _P]),
     "tp_viterbi_workspace_bytes": (_I64, [_I64, _I64]),
     "tp_tcq_viterbi": (c_int, [_P, _I64, _I64, _I64, _P, c_int, c_int, _P, _P, _P, _P, _P, _P, _I64, _P]),

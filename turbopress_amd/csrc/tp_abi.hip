@@ -37,15 +37,6 @@ extern "C" int tp_subset_lut(int n_states, uint8_t* lut_out, int lut_len) {
   return TP_OK;
 }
 
-// Bounded busy-wait kernel for benchmarking: keeps the stream busy for about
-// `microseconds` (measured on the GPU's constant wall clock) so that a host can
-// enqueue a run of kernels ahead of the GPU and events time them without
-// host submission gaps.  Capped at one second; always terminates.
-__global__ void tp_delay_kernel(uint64_t ticks) {
-  const uint64_t t0 = wall_clock64();
-  while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(64);
-}
-
 // Streaming read of `n16` 16-byte words: grid-stride, eight loads in flight
 // per thread, XOR-folded so that nothing is elided; one word is stored only
 // when the fold hits an arbitrary constant (practically never).
@@ -74,16 +65,5 @@ extern "C" int tp_read_probe(const void* buf, int64_t bytes, uint32_t* sink, voi
   const int grid = 4 * tp::device_cu_count();  // 4 workgroups of 512 threads per CU
   hipLaunchKernelGGL(tp_read_probe_kernel, dim3(grid), dim3(512), 0, (hipStream_t)stream,
                      reinterpret_cast<const probe_v4*>(buf), (uint64_t)bytes / 16u, sink);
-  return tp::launch_status();
-}
-
-extern "C" int tp_device_delay(int64_t microseconds, void* stream) {
-  if (microseconds < 0 || microseconds > 1000000) return TP_ERR_BAD_DIMS;
-  int dev = 0, khz = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0)
-    khz = 100000;  // 100 MHz, the gfx9 constant wall clock
-  const uint64_t ticks = (uint64_t)microseconds * (uint64_t)khz / 1000u;
-  hipLaunchKernelGGL(tp_delay_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, ticks);
   return tp::launch_status();
 }

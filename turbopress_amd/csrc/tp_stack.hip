@@ -45,8 +45,13 @@
 namespace tp {
 
 constexpr int kStackMaxPhases = 4096;
-constexpr int kStackMaxLinears = 4096;       // schedule entries: (linear << 20) | block
-constexpr int kStackBlockBits = 20;
+// Schedule entries are int32 values (linear << kStackBlockBits) | block: a
+// plan holds at most 2^16 linears of at most 2^14 blocks each (2M rows), so
+// every entry stays positive.
+constexpr int kStackBlockBits = 14;
+constexpr int kStackMaxLinears = 1 << 16;
+static_assert(((int64_t)kStackMaxLinears << kStackBlockBits) - 1 <= INT32_MAX,
+              "schedule entries must fit a positive int32");
 // Batches up to this use the slot kernel (4 batch rows per slot); larger ones
 // the wide kernel, which at batch 8 measured 371 us per Qwen3-4B step
 // against 475 us for 2 slots of 8 rows (whose z registers leave room for only

@@ -288,7 +288,3 @@ def forward_group(layers, x: Tensor) -> list:
         _lib.check(st, "packed_linear_forward_group")
     return [o.reshape(*x.shape[:-1], o.shape[1]) for o in outs]
 
-
-def device_delay(microseconds: int, device=None) -> None:
-    """Enqueue a bounded busy-wait kernel on the current stream (benchmarks)."""
-    _lib.check(_lib.lib().tp_device_delay(int(microseconds), current_stream_ptr(device)), "device_delay")

@@ -74,9 +74,7 @@ def make_payload(n: int, d: int, bits: int, n_states: int = 64, seed: int = 0,
     """A seeded format-v2 payload of an n x d packed linear (CPU tensors)."""
     if bits < 1 or bits > 7:
         raise ValueError(f"bits must be in [1, 7], got {bits}")
-    block = d & -d
-    if block < 2:
-        raise ValueError(f"in_features={d} has no power-of-2 factor")
+    block = d & -d  # hadamard.py:30-34; 1 for odd d (the rotation is then the identity)
     gen = torch.Generator().manual_seed(seed)
     path = torch.randint(0, 256, (n, (d + 7) // 8), generator=gen, dtype=torch.uint8)
     _mask_row_padding(path, d)
