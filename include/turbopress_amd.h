@@ -188,6 +188,23 @@ int tp_packed_linear_forward(const uint16_t* x, int64_t ldx, int64_t batch,
                              int n_states, uint16_t* y, int64_t ldy, void* workspace,
                              int64_t workspace_bytes, void* stream);
 
+/* tp_packed_linear_forward without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The split-K workspace (batch 5..32) is a fixed device array inside the
+ * library, one per GPU, held until the process ends: n up to 16384 rows at
+ * any batch <= 32 (32768 at batch <= 16); larger calls return
+ * TP_ERR_WORKSPACE.  Each call clears the part it uses (a small fill kernel)
+ * and allocates nothing.  The first call on a device looks the array up
+ * (not capturable: make one call per device before capturing).  Calls that
+ * overlap on one GPU race. */
+int tp_packed_linear_forward_noalloc(const uint16_t* x, int64_t ldx, int64_t batch,
+                                     const uint16_t* rot_scale, int64_t block,
+                                     const uint8_t* path_tiled, const uint8_t* member_tiled,
+                                     const uint16_t* scales, const uint16_t* codebook,
+                                     const uint16_t* bias, int64_t n, int64_t d, int bits,
+                                     int n_states, uint16_t* y, int64_t ldy, void* stream);
+
 /* One launch for up to 4 packed linears that read the same input x (e.g. the
  * q/k/v or gate/up projections of a decoder layer) and share one codebook:
  * each has its own rot_scale/block, streams, scales, bias (array may be NULL),

@@ -98,6 +98,17 @@ def test_stack_plan_size_limits(built_lib):
     assert built_lib.tp_stack_plan_bytes(_stack_array(1), 1, 3, 33) == 0
 
 
+def test_noalloc_rejects_calls_beyond_its_array(built_lib):
+    """The no-allocation forward refuses, on the host, a call whose split-K
+    workspace would exceed its fixed device array (16384 rows at batch 32)."""
+    from turbopress_amd import _lib
+    fake = ctypes.c_void_p(256)
+    args = [fake, 256, 32, fake, 256, fake, fake, fake, fake, None, 16400, 256, 3, 64, fake, 16400, None]
+    assert built_lib.tp_packed_linear_forward_noalloc(*args) == _lib.TP_ERR_WORKSPACE
+    args[2] = 33
+    assert built_lib.tp_packed_linear_forward_noalloc(*args) == _lib.TP_ERR_BAD_DIMS
+
+
 def test_check_maps_status_to_reference_exceptions():
     from turbopress_amd import _lib
     with pytest.raises(ValueError):

@@ -50,6 +50,8 @@ SIGNATURES: dict[str, tuple] = {
     "tp_decode_tiled": (c_int, [_P, _P, _P, _P, _I64, _I64, c_int, c_int, _P, _I64, _P]),
     "tp_packed_linear_forward": (c_int, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64,
                                          c_int, c_int, _P, _I64, _P, _I64, _P]),
+    "tp_packed_linear_forward_noalloc": (c_int, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64,
+                                                 c_int, c_int, _P, _I64, _P]),
     "tp_packed_linear_forward_group": (c_int, [c_int, _P, _I64, _I64, _P, _P, _P, _P, _P, _P, _P, _P,
                                                _I64, c_int, c_int, _P, _P, _P, _P, _P]),
 }
