@@ -263,7 +263,10 @@ int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears, int bits,
  * input into the plan's z buffer and ONE persistent launch runs all GEMVs
  * (batch <= 4: the slot kernel; 5..32: the wide kernel).  With
  * ordered != 0 a linear of phase p starts only after all linears of phase
- * p-1 finished.  The plan's counters return to zero after each run, so one
+ * p-1 finished (their y stores complete).  Ordering schedules work; it does
+ * not pass data: every input is rotated by the first launch, before any
+ * phase runs, so a phase cannot consume an earlier phase's outputs within
+ * one run.  The plan's counters return to zero after each run, so one
  * plan serves any number of runs or graph replays on one stream (runs that
  * overlap on one plan race).  Sizes are read from the plan; `batch` (the
  * plan's batch) and total_blocks (tp_stack_plan_blocks) only size the launch.

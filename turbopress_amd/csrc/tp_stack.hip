@@ -63,7 +63,8 @@ constexpr int kSlotMaxBatch = 4;
 //   [64, ...)           StackInfo, RotItem[n_rot] (at the fixed offset
 //                       kRotItems), LinearDesc[n_lin], prefix[n_lin+1],
 //                       lphase[n_lin], pblocks[n_phases], sched_ordered[total],
-//                       sched_unordered[total]  -- read-only
+//                       sched_unordered[total], wide schedules, ptiles[n_phases],
+//                       ord_blocks[<= 8 total]  -- read-only
 //   [pdone, ...)        pdone[n_phases] -- written by the kernel (atomics)
 //   [zbuf, ...)         rotated activations
 // The read-only part is passed as a separate const __restrict__ argument so
@@ -72,7 +73,8 @@ struct StackCounters {
   uint32_t ticket;   // next block index (reset to 0 by the last workgroup out)
   uint32_t exited;   // workgroups past the loop (reset likewise)
   uint32_t error;    // 1: a phase wait timed out; 2: launched for fewer batch rows than the plan
-  uint32_t reserved[13];
+  uint32_t gen;      // ordered kernel: launches finished (phase counters count on across launches)
+  uint32_t reserved[12];
 };
 
 struct StackInfo {
@@ -84,7 +86,7 @@ struct StackInfo {
   int32_t min_g4;         // shortest K of the plan in 256-column units
   int64_t zbuf_bytes;
   int32_t total_wide;     // wide blocks (16 tiles x full K) of the batch 5..32 kernel
-  int32_t reserved;
+  int32_t total_k;        // blocks of the ordered kernel (tile groups with K split across the waves)
 };
 
 // One rotation tile (4096 columns of one batch row of one linear's input),
@@ -104,9 +106,22 @@ struct RotItem {
 };
 static_assert(sizeof(RotItem) == 64, "one 16-dword scalar load per rotation tile");
 
-struct StackLayout {
-  size_t rot_items, lin, prefix, lphase, pblocks, sched_o, sched_u, sched_wo, sched_wu, pdone, zbuf, total;
+// One block of the ordered kernel: row tiles [t0, t0 + nt) of linear li.
+struct OrdBlockDesc {
+  int32_t li, t0, nt, reserved;
 };
+static_assert(sizeof(OrdBlockDesc) == 16, "one 4-dword scalar load per block");
+
+struct StackLayout {
+  size_t rot_items, lin, prefix, lphase, pblocks, sched_o, sched_u, sched_wo, sched_wu, ptiles, oblk, pdone,
+      odone, zbuf, total;
+};
+
+// Ordered kernel: every phase counter is kept in kOrdReplicas copies on
+// separate 128-byte lines (each workgroup adds its tiles to all of them and
+// polls one), so that hundreds of waiting workgroups do not all poll one line.
+constexpr int kOrdReplicas = 16;
+constexpr int kOrdLineWords = 32;
 
 constexpr size_t kStackRO = sizeof(StackCounters);
 constexpr size_t kRotItems = (kStackRO + sizeof(StackInfo) + 63) & ~(size_t)63;  // fixed offset
@@ -143,9 +158,16 @@ __host__ __device__ inline StackLayout stack_layout(int n_lin, int n_phases, int
   o += sizeof(int32_t) * (size_t)total_blocks;
   p.sched_wu = o;
   o += sizeof(int32_t) * (size_t)total_blocks;
+  p.ptiles = o;
+  o += sizeof(int32_t) * (size_t)n_phases;
+  p.oblk = o;  // ordered kernel: at most one block per row tile (8 per 8-tile block)
+  o += sizeof(OrdBlockDesc) * (size_t)total_blocks * 8;
   o = (o + 63) & ~(size_t)63;
   p.pdone = o;
   o += sizeof(uint32_t) * (size_t)n_phases;
+  o = (o + 127) & ~(size_t)127;
+  p.odone = o;
+  o += sizeof(uint32_t) * (size_t)n_phases * kOrdReplicas * kOrdLineWords;
   o = (o + 255) & ~(size_t)255;
   p.zbuf = o;
   o += (size_t)zbuf_bytes;
@@ -163,7 +185,10 @@ struct StackRO {  // views into the read-only part
   const int32_t* sched_u;  // [total] same blocks, longest K first
   const int32_t* sched_wo; // [total_wide] (linear << 20) | wide block, phase order
   const int32_t* sched_wu; // [total_wide] same, longest K first
+  const int32_t* ptiles;   // [n_phases] row tiles per phase
+  const OrdBlockDesc* oblk;  // [total_k] ordered-kernel blocks, phase order
   size_t pdone;            // byte offset of pdone from the plan start
+  size_t odone;            // byte offset of the ordered kernel's replicated phase counters
   size_t zbuf;             // byte offset of the z buffer from the plan start
 };
 
@@ -182,7 +207,10 @@ __device__ inline StackRO stack_ro(const char* __restrict__ ro) {
   v.sched_u = reinterpret_cast<const int32_t*>(ro + (l.sched_u - kStackRO));
   v.sched_wo = reinterpret_cast<const int32_t*>(ro + (l.sched_wo - kStackRO));
   v.sched_wu = reinterpret_cast<const int32_t*>(ro + (l.sched_wu - kStackRO));
+  v.ptiles = reinterpret_cast<const int32_t*>(ro + (l.ptiles - kStackRO));
+  v.oblk = reinterpret_cast<const OrdBlockDesc*>(ro + (l.oblk - kStackRO));
   v.pdone = l.pdone;
+  v.odone = l.odone;
   v.zbuf = l.zbuf;
   return v;
 }
@@ -665,6 +693,401 @@ tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
 }
 
 // ---------------------------------------------------------------------------
+// 2b. ordered kernel (batch <= 4, the decoder's phase order enforced)
+// ---------------------------------------------------------------------------
+// A linear of phase p may start only after every linear of phase p - 1 has
+// finished.  Most phases hold far less work than the chip (one Qwen3-4B
+// layer, in units of 16 rows x 256 columns: q/k/v 3840, o 2560, gate/up
+// 12160, down 6080; 4096 waves), so a phase costs its latency chain: phase
+// wait, decode, the sum over K, the y stores and the count.  The plan
+// therefore cuts each phase into at most `grid` blocks where shapes allow
+// (whole row tiles of one linear, balanced by units), so that a workgroup
+// holds about one block per phase.  A block's units, tile-major, are split
+// into 8 contiguous chunks, one per wave (a chunk spans at most 4 tiles); a
+// wave loads the first units of its chunk, its halo word and the scales of
+// the tiles it finishes BEFORE the phase wait, while the previous phase is
+// still running, and streams the rest of the chunk through the same
+// registers.  Per-tile partial sums go through LDS and are added in wave
+// order (deterministic); wave w finishes tiles w, w + 8 and w + 16.  Blocks
+// are handed out by index in phase order (block b to workgroup b % grid):
+// every block a workgroup waits on was handed to a workgroup that reaches it
+// first, so the waits always end.  The phase counters count finished row
+// tiles.
+
+// Tiles per block: a wave's chunk, ceil(nt * G4 / 8) <= 3 * G4 units, then
+// spans at most kOrdSegs tiles; every wave finishes kOrdFinish of them.
+constexpr int kOrdMaxTiles = 24;
+constexpr int kOrdSegs = 4;
+constexpr int kOrdFinish = kOrdMaxTiles / kWavesPerGroup;
+static_assert(kOrdFinish * kWavesPerGroup == kOrdMaxTiles, "tiles finished per wave");
+
+// Units of a wave's chunk held in registers at once (4 bits: the member
+// words take the registers of the fourth).
+__host__ __device__ constexpr int ord_max_units(int bits) { return bits == 4 ? 3 : 4; }
+
+// Blocks of the ordered kernel for the linears [i0, i1) of one phase: at
+// most `grid` where kOrdMaxTiles tiles per block allow, sized by units.
+inline int64_t ord_phase_blocks(const LinearDesc* lin, int i0, int i1, int grid, OrdBlockDesc* out) {
+  int64_t units = 0;
+  for (int i = i0; i < i1; ++i) units += (int64_t)lin[i].T * lin[i].G4;
+  // tiles per block of linear i for a target of tg units per block (and at
+  // most 2^21 units per block, so that byte offsets stay 32-bit)
+  auto tpb = [&](int i, int64_t tg) {
+    const int64_t cap = std::max<int64_t>(1, std::min<int64_t>(kOrdMaxTiles, ((int64_t)1 << 21) / lin[i].G4));
+    return (int)std::min<int64_t>(cap, std::max<int64_t>(1, tg / lin[i].G4));
+  };
+  auto count = [&](int64_t tg) {
+    int64_t c = 0;
+    for (int i = i0; i < i1; ++i) c += (lin[i].T + tpb(i, tg) - 1) / tpb(i, tg);
+    return c;
+  };
+  auto capped = [&](int64_t tg) {
+    for (int i = i0; i < i1; ++i)
+      if (tpb(i, tg) < tpb(i, (int64_t)1 << 40)) return false;
+    return true;
+  };
+  int64_t tg = std::max<int64_t>(1, (units + grid - 1) / grid);
+  while (count(tg) > grid && !capped(tg)) tg += std::max<int64_t>(1, tg / 16);
+  int64_t nb = 0;
+  for (int i = i0; i < i1; ++i) {
+    const int t = tpb(i, tg);
+    for (int t0 = 0; t0 < lin[i].T; t0 += t) out[nb++] = {i, t0, std::min(t, lin[i].T - t0), 0};
+  }
+  return nb;
+}
+
+// Bounded wait of one thread until every row tile of phase ph - 1 has
+// finished in this launch: replica r of the phase's counter has reached
+// (gen + 1) * tiles (counters count on across launches, modulo 2^32).
+__device__ inline void wait_phase_replica(const StackRO& P, const uint32_t* odone, StackCounters* C, int ph,
+                                          uint32_t gen, int r, int spin_limit) {
+  const uint32_t need = (gen + 1u) * (uint32_t)cread(P.ptiles + ph - 1);
+  const uint32_t* ctr = odone + ((size_t)(ph - 1) * kOrdReplicas + r) * kOrdLineWords;
+  int spins = 0;
+  while ((int32_t)(__hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - need) < 0) {
+    if (++spins > spin_limit) {
+      atomicExch(&C->error, 1u);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(4);
+  }
+}
+
+// Add `tiles` finished tiles of phase ph to every replica of its counter
+// (no return value: nothing waits for these atomics).
+__device__ inline void count_phase_tiles(uint32_t* odone, int ph, uint32_t tiles) {
+  uint32_t* ctr = odone + (size_t)ph * kOrdReplicas * kOrdLineWords;
+#pragma unroll
+  for (int r = 0; r < kOrdReplicas; ++r)
+    __hip_atomic_fetch_add(ctr + r * kOrdLineWords, tiles, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Where one block of the ordered schedule sits, and the wave's chunk of it
+// (scalar values, read one block ahead).
+struct OrdDesc {
+  bool valid;
+  int li, t0, nt, G4, N, ph;
+  int c0, nu;  // the wave's chunk: flat units [c0, c0 + nu) of the block
+  int tc, k0;  // tile and K unit of flat unit c0
+  __amdgpu_buffer_rsrc_t prs, mrs, srs;
+  uint32_t zoff, zld;
+  const uint16_t* bias;
+  uint16_t* y;
+  int n, ldy;
+};
+
+template <int MW>
+__device__ __forceinline__ OrdDesc ord_desc(const StackRO& P, int blk, int total, int wave, const char* zbuf) {
+  constexpr uint32_t unit_p = 4u * kTileRows * 8u;
+  constexpr uint32_t unit_m = 4u * kTileRows * MW * 4u;
+  OrdDesc D;
+  D.valid = blk < total;
+  const TP_CONST OrdBlockDesc& E = cread(P.oblk + (D.valid ? blk : 0));
+  D.li = E.li;
+  D.t0 = E.t0;
+  D.nt = D.valid ? E.nt : 0;
+  const TP_CONST LinearDesc& L = cread(P.lin + D.li);
+  D.G4 = L.G4;
+  D.N = D.nt * D.G4;
+  D.c0 = (wave * D.N) >> 3;  // 8 waves
+  D.nu = (((wave + 1) * D.N) >> 3) - D.c0;
+  D.tc = D.c0 / D.G4;
+  D.k0 = D.c0 - D.tc * D.G4;
+  D.ph = cread(P.lphase + D.li);
+  D.prs = buffer_rsrc(reinterpret_cast<const char*>(L.path) + (size_t)D.t0 * D.G4 * unit_p,
+                      (uint32_t)D.N * unit_p);
+  D.mrs = buffer_rsrc(reinterpret_cast<const char*>(L.member) + (size_t)D.t0 * D.G4 * unit_m,
+                      (uint32_t)D.N * unit_m);
+  D.srs = buffer_rsrc(L.scales, (uint32_t)L.n * 2u);
+  D.zoff = (uint32_t)(reinterpret_cast<const char*>(L.z) - zbuf);
+  D.zld = (uint32_t)D.G4 * kChunkCols;
+  D.bias = L.bias;
+  D.y = L.y;
+  D.n = L.n;
+  D.ldy = L.ldy;
+  return D;
+}
+
+// Registers of one block: UMAX units in flight (a rolling window over the
+// wave's chunk), the halo word (path word 1 of the unit before the chunk,
+// K block 3 lanes) and the row scales of the tiles the wave finishes.
+template <int MW, int NZ, int UMAX>
+struct OrdRegs {
+  UnitRegs<MW, NZ> R[UMAX];
+  uint32_t x1_prev;
+  u32x2_t sc[kOrdFinish];
+};
+
+// Loads of flat unit f (K unit k) of the block into R (past the wave's
+// chunk: out of range, no memory traffic).  zv: the lane's z offsets inside
+// a unit (out of range for batch rows past the batch).
+template <int MW, int NZ>
+__device__ __forceinline__ void ord_unit(UnitRegs<MW, NZ>& R, const OrdDesc& D, int f, int k, uint32_t pv,
+                                         uint32_t mv, const uint32_t* zv, __amdgpu_buffer_rsrc_t zrs) {
+  constexpr uint32_t unit_p = 4u * kTileRows * 8u;
+  constexpr uint32_t unit_m = 4u * kTileRows * MW * 4u;
+  constexpr uint32_t unit_z = kChunkCols * 2u;
+  const bool ok = f < D.c0 + D.nu;
+  const uint32_t fu = (uint32_t)(ok ? f : 0), ku = (uint32_t)(ok ? k : 0);
+  R.X = __builtin_amdgcn_raw_buffer_load_b64(D.prs, ok ? pv : kOutOfRange, fu * unit_p, weight_policy(MW));
+  R.M = MemberBuf<MW>::load(D.mrs, ok ? mv : kOutOfRange, fu * unit_m);
+#pragma unroll
+  for (int l = 0; l < NZ; ++l)
+    R.Z[l] = __builtin_amdgcn_raw_buffer_load_b128(zrs, ok ? zv[l] : kOutOfRange, D.zoff + ku * unit_z, 0);
+}
+
+// K unit after k in a tile of G4 units (wrapping to the next tile).
+__device__ __forceinline__ int ord_next_k(int k, int G4) { return k + 1 == G4 ? 0 : k + 1; }
+
+// A block's first loads: halo word and scales (oldest, so that waiting for
+// them waits for nothing else of the block), then the chunk's first UMAX
+// units.
+template <int MW, int NZ, int UMAX>
+__device__ __forceinline__ void ord_head(OrdRegs<MW, NZ, UMAX>& B, const OrdDesc& D, int wave, uint32_t pv,
+                                         uint32_t mv, const uint32_t* zv, int q, __amdgpu_buffer_rsrc_t zrs) {
+  constexpr uint32_t unit_p = 4u * kTileRows * 8u;
+  B.x1_prev = __builtin_amdgcn_raw_buffer_load_b32(D.prs, (D.nu > 0 && D.k0 > 0) ? pv + 4u : kOutOfRange,
+                                                   (uint32_t)(D.k0 > 0 ? D.c0 - 1 : 0) * unit_p, 0);
+#pragma unroll
+  for (int i = 0; i < kOrdFinish; ++i) {
+    const int t = wave + i * kWavesPerGroup;
+    B.sc[i] = __builtin_amdgcn_raw_buffer_load_b64(
+        D.srs, t < D.nt ? ((uint32_t)(D.t0 + t) * kTileRows + 4u * (uint32_t)q) * 2u : kOutOfRange, 0, 0);
+  }
+  int k = D.k0;
+#pragma unroll
+  for (int u = 0; u < UMAX; ++u) {
+    ord_unit<MW, NZ>(B.R[u], D, D.c0 + u, k, pv, mv, zv, zrs);
+    k = ord_next_k(k, D.G4);
+  }
+}
+
+// Vector memory operations ord_head issues: 2 + NZ per unit (3 + NZ at 4
+// bits), the halo word and the scales.
+__host__ __device__ constexpr int ord_loads(int bits, int nz, int umax) {
+  return (bits == 4 ? 3 + nz : 2 + nz) * umax + 1 + kOrdFinish;
+}
+
+// The lane's z offsets inside a unit of a block (batch rows past the batch:
+// out of range).
+template <int NZ>
+__device__ __forceinline__ void ord_zv(uint32_t* zv, const OrdDesc& D, int q, int slot, int bb, int batch) {
+  constexpr int SLOTS = 4;
+#pragma unroll
+  for (int l = 0; l < NZ; ++l)
+    zv[l] = bb < batch ? ((uint32_t)bb * D.zld + (uint32_t)(q * kSegCols + mfma_col(l * SLOTS + slot))) * 2u
+                       : kOutOfRange;
+}
+
+// A wave's partial sum of one tile into LDS: accumulator `slot` holds this
+// lane's column; the slots of each batch row are summed and the 16 (K
+// block, batch row) sums land in the slot-0 lanes.
+template <int SLOTS, int SB>
+__device__ __forceinline__ void ord_flush(float4_t* acc, float4_t* dst, uint32_t slot_bit, int slot, int pl) {
+  float4_t v = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < SLOTS; ++k) {
+    const float msk = (float)__builtin_amdgcn_ubfe(slot_bit, (uint32_t)k, 1u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(acc[k][i], msk, v[i]);
+    acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int w = SB; w < 16; w <<= 1)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], w, 64);
+  if (slot == 0) dst[pl] = v;
+}
+
+template <int KB, int NS>
+__global__ void __launch_bounds__(kGroupThreads) __attribute__((amdgpu_waves_per_eu(4)))
+tcq_stack_ordered_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
+                         const uint16_t* __restrict__ codebook, int spin_limit) {
+  constexpr int SB = 4, SLOTS = 4, NZ = 2;
+  constexpr int MW = member_words(KB);
+  constexpr int UMAX = ord_max_units(KB);
+  __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
+  // partial sums: [wave][tile % kOrdSegs][(K block, batch row)]
+  __shared__ __attribute__((aligned(16))) float4_t part[kWavesPerGroup][kOrdSegs][16];
+  const StackRO P = stack_ro(plan_ro);
+  const TP_CONST StackInfo& info = cread(P.info);
+  StackCounters* C = reinterpret_cast<StackCounters*>(plan_rw);
+  uint32_t* odone = reinterpret_cast<uint32_t*>(plan_rw + P.odone);
+  const int batch = info.batch;
+  const int total = info.total_k;
+  if (batch > SB || info.n_rot <= 0) {  // not a plan for this kernel: refuse uniformly
+    if (threadIdx.x == 0 && blockIdx.x == 0) atomicExch(&C->error, 2u);
+    return;
+  }
+  const char* zbuf = plan_rw + P.zbuf;
+  const __amdgpu_buffer_rsrc_t zrs = buffer_rsrc(zbuf, (uint32_t)info.zbuf_bytes);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & 15, q = lane >> 4;
+  const int slot = r / SB, bb = r % SB;
+  const int pl = q * 4 + bb;  // this lane's (K block, batch row) sum in the slot-0 lanes
+  const uint32_t slot_bit = 1u << slot;
+  const uint32_t laneoff = lane_offsets<KB>(lane);
+  const uint32_t pv = (uint32_t)(q * kTileRows + r) * 8u;
+  const uint32_t mv = (uint32_t)(q * kTileRows + r) * MW * 4u;
+  const uint32_t cb_lane = gld(codebook + (lane & ((2 << KB) - 1)));
+  const int rep = (int)blockIdx.x % kOrdReplicas;
+  uint32_t gen = 0;
+  if (tid == 0) gen = __hip_atomic_load(&C->gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  int blk = blockIdx.x;
+  OrdDesc D = ord_desc<MW>(P, blk, total, wave, zbuf);
+  OrdRegs<MW, NZ, UMAX> B;
+  uint32_t zv[NZ];
+  ord_zv<NZ>(zv, D, q, slot, bb, batch);
+  if (D.valid) ord_head<MW, NZ, UMAX>(B, D, wave, pv, mv, zv, q, zrs);
+  OrdDesc Dn = ord_desc<MW>(P, blk + gridDim.x, total, wave, zbuf);
+  build_pair_table_lanes<KB>(table, cb_lane, tid, kGroupThreads);
+  uint32_t done_tiles = 0;  // thread 0: tiles of phase D.ph finished, not yet counted
+  int open_ph = 0;          // phases up to this one are open to this workgroup
+
+  while (D.valid) {
+    if (D.ph > open_ph) {  // (a workgroup's blocks come in phase order)
+      if (tid == 0) wait_phase_replica(P, odone, C, D.ph, gen, rep, spin_limit);
+      open_ph = D.ph;
+    }
+    __syncthreads();  // (also: the last block's reads of `part` are done)
+    float4_t acc[SLOTS];
+#pragma unroll
+    for (int k = 0; k < SLOTS; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
+    // The chunk through a rolling window of UMAX register sets: the first
+    // UMAX units were loaded before the phase wait; in longer chunks the set
+    // a unit frees is reloaded with the unit UMAX further on.  A tile that
+    // ends inside the chunk leaves its partial sum in LDS.
+    uint32_t prev = B.x1_prev;
+    int kd = D.k0, td = D.tc;  // K unit and tile of the unit decoded next
+    int kl = D.k0;             // K unit of the unit reloaded next
+#pragma unroll
+    for (int u = 0; u < UMAX; ++u) kl = ord_next_k(kl, D.G4);
+    for (int base = 0; base < D.nu; base += UMAX) {
+      const bool more = base + UMAX < D.nu;  // (wave-uniform)
+#pragma unroll
+      for (int u = 0; u < UMAX; ++u) {
+        if (base + u < D.nu) {
+          if (kd == 0) prev = 0u;  // a tile starts: no halo
+          const uint32_t provide = (q == 3) ? prev : B.R[u].X[1];
+          slot_unit<KB, NS, SB, MW, NZ>(B.R[u], provide, lane, laneoff, table, acc);
+          prev = B.R[u].X[1];
+          kd = ord_next_k(kd, D.G4);
+          if (kd == 0) ord_flush<SLOTS, SB>(acc, part[wave][td++ % kOrdSegs], slot_bit, slot, pl);
+        }
+        if (more) {
+          ord_unit<MW, NZ>(B.R[u], D, D.c0 + base + UMAX + u, kl, pv, mv, zv, zrs);
+          kl = ord_next_k(kl, D.G4);
+        }
+      }
+    }
+    if (D.nu > 0 && kd != 0) ord_flush<SLOTS, SB>(acc, part[wave][td % kOrdSegs], slot_bit, slot, pl);
+    // Every load of the block has been consumed or was out of range (those
+    // return at once): an explicit wait tells the compiler so, and keeps its
+    // own waits out of the y stores and the next block's loads below.
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+    __syncthreads();
+    // Wave w finishes tiles w, w + 8, w + 16: the partial sums of the waves
+    // whose chunks meet the tile, in wave order.
+#pragma unroll
+    for (int i = 0; i < kOrdFinish; ++i) {
+      const int t = wave + i * kWavesPerGroup;
+      if (t < D.nt && slot == 0) {
+        float4_t v = float4_t{0.f, 0.f, 0.f, 0.f};
+        const int ta = t * D.G4, tb = ta + D.G4;  // the tile's flat units
+        for (int w = 0; w < kWavesPerGroup; ++w) {
+          const int a = (w * D.N) >> 3, b = ((w + 1) * D.N) >> 3;
+          if (a < b && a < tb && b > ta) {
+            const float4_t s = part[w][t % kOrdSegs][pl];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[j] += s[j];
+          }
+        }
+        if (bb < batch) {
+          const int row0 = (D.t0 + t) * kTileRows + 4 * q;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int row = row0 + j;
+            if (row >= D.n) continue;
+            uint16_t out = f2h(v[j] * h2f((uint16_t)(B.sc[i][j >> 1] >> (16 * (j & 1)))));
+            if (D.bias) out = f2h(h2f(out) + h2f(gld(D.bias + row)));
+            gst(D.y + (size_t)bb * D.ldy + row, out);
+          }
+        }
+      }
+    }
+    // The next block's loads go out at once when it belongs to this phase or
+    // the next one.  For a later phase they wait until the phase before it
+    // is open: all workgroups end a phase together, and loads for far-off
+    // phases issued then would queue ahead of the stores and loads of the
+    // phases that run first.
+    const bool near = Dn.valid && Dn.ph <= D.ph + 1;
+    if (near) {
+      ord_zv<NZ>(zv, Dn, q, slot, bb, batch);
+      ord_head<MW, NZ, UMAX>(B, Dn, wave, pv, mv, zv, q, zrs);
+    }
+    if (tid == 0) done_tiles += (uint32_t)D.nt;
+    if (!Dn.valid || Dn.ph != D.ph) {
+      // Last block of the phase in this workgroup: count its tiles once the
+      // y stores of every wave are complete.  A near block's loads are
+      // already out; the stores are complete once no more than those loads
+      // are outstanding (loads and stores complete in order).
+      if (near)
+        __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(ord_loads(KB, NZ, UMAX)) : "memory");
+      else
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (tid == 0) {
+        count_phase_tiles(odone, D.ph, done_tiles);
+        done_tiles = 0;
+      }
+    }
+    if (Dn.valid && !near) {
+      if (tid == 0) wait_phase_replica(P, odone, C, Dn.ph - 1, gen, rep, spin_limit);
+      __syncthreads();
+      ord_zv<NZ>(zv, Dn, q, slot, bb, batch);
+      ord_head<MW, NZ, UMAX>(B, Dn, wave, pv, mv, zv, q, zrs);
+    }
+    D = Dn;
+    blk += gridDim.x;
+    Dn = ord_desc<MW>(P, blk + gridDim.x, total, wave, zbuf);
+  }
+
+  // The last workgroup out resets the launch counters and opens the next
+  // launch's generation.
+  if (tid == 0) {
+    const uint32_t ex = atomicAdd(&C->exited, 1u);
+    if (ex == gridDim.x - 1) {
+      atomicExch(&C->ticket, 0u);
+      atomicExch(&C->exited, 0u);
+      atomicAdd(&C->gen, 1u);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 3. wide kernel (stack: batch 5..32; one linear: batch 9..32)
 // ---------------------------------------------------------------------------
 // One workgroup of 16 waves per CU takes *wide blocks* (16 row tiles x the
@@ -1100,7 +1523,7 @@ int linear_forward_wide(const LinearDesc& Lin, const uint16_t* z, int64_t zld, i
 // rotation tile count, blocks, batch and layout offsets.  A plan the process
 // did not initialise gets kernels that read these from the plan header.
 struct PlanReg {
-  int n_rot, total, batch;
+  int n_rot, total, batch, total_k;
   int64_t lin_off, sched_o_off, sched_u_off;
 };
 std::mutex g_plan_mutex;
@@ -1119,12 +1542,18 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
                 int spin_limit, hipStream_t s) {
   const char* ro = plan + kStackRO;
   const int cus = device_cu_count();
-  if (batch <= kSlotMaxBatch) {
+  PlanReg reg;
+  const bool known = plan_lookup(plan, &reg) && reg.batch == batch && reg.total == total_blocks;
+  if (ordered && batch <= kSlotMaxBatch) {
+    // phase order enforced: tile groups with K split across the waves
+    const int total_k = known ? reg.total_k : 0;
+    const int grid = total_k > 0 ? std::min(total_k, cus * 2) : cus * 2;
+    hipLaunchKernelGGL((tcq_stack_ordered_kernel<KB, NS>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
+                       spin_limit);
+  } else if (batch <= kSlotMaxBatch) {
     const int grid = (int)(total_blocks < (int64_t)cus * 2 ? total_blocks : (int64_t)cus * 2);
     PlanArgs pa = {0, 0, 0, 0};
-    PlanReg reg;
-    if (plan_lookup(plan, &reg) && reg.batch == batch && reg.total == total_blocks)
-      pa = {reg.lin_off, ordered ? reg.sched_o_off : reg.sched_u_off, reg.total, reg.batch};
+    if (known) pa = {reg.lin_off, ordered ? reg.sched_o_off : reg.sched_u_off, reg.total, reg.batch};
     hipLaunchKernelGGL((tcq_stack_slot_kernel<KB, NS, 4>), dim3(grid), dim3(kGroupThreads), 0, s, ro, plan, cb,
                        ordered, spin_limit, pa);
   } else {
@@ -1213,6 +1642,9 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
   int32_t* sched_u = reinterpret_cast<int32_t*>(host + lay.sched_u);
   int32_t* sched_wo = reinterpret_cast<int32_t*>(host + lay.sched_wo);
   int32_t* sched_wu = reinterpret_cast<int32_t*>(host + lay.sched_wu);
+  int32_t* ptiles = reinterpret_cast<int32_t*>(host + lay.ptiles);
+  OrdBlockDesc* oblk = reinterpret_cast<OrdBlockDesc*>(host + lay.oblk);
+  int64_t total_k = 0;
   RotItem* items = reinterpret_cast<RotItem*>(host + lay.rot_items);
   char* zbuf = reinterpret_cast<char*>(plan) + lay.zbuf;
   int64_t total = 0, rot = 0, zoff = 0;
@@ -1258,6 +1690,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     lphase[i] = l.phase;
     pblocks[l.phase] += L.blocks;
     for (int b = 0; b < L.blocks; ++b) sched_o[total + b] = (i << kStackBlockBits) | b;
+    ptiles[l.phase] += L.T;
     total += L.blocks;
     if (z.zbuf_bytes) {
       const int ntiles = rot_tiles((int)g.G4);
@@ -1295,7 +1728,17 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     int64_t kw = 0;
     for (int i : order)
       for (int b = 0; b < (lin[i].T + kWideWaves - 1) / kWideWaves; ++b) sched_wu[kw++] = (i << kStackBlockBits) | b;
+    // Ordered-kernel blocks, phase by phase (a phase's linears are
+    // consecutive), sized for the slot-kernel grid of this device.
+    const int grid = 2 * device_cu_count();
+    for (int i0 = 0; i0 < n_linears;) {
+      int i1 = i0 + 1;
+      while (i1 < n_linears && lphase[i1] == lphase[i0]) ++i1;
+      total_k += ord_phase_blocks(lin, i0, i1, grid, oblk + total_k);
+      i0 = i1;
+    }
     h->total_wide = (int32_t)nw;
+    h->total_k = (int32_t)total_k;
     h->n_lin = n_linears;
     h->total_blocks = (int32_t)total;
     h->n_phases = z.n_phases;
@@ -1308,7 +1751,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
   {
     std::lock_guard<std::mutex> lock(g_plan_mutex);
     if (st == TP_OK && z.n_rot > 0)
-      g_plans[plan] = {(int)z.n_rot, (int)total, (int)batch, (int64_t)(lay.lin - kStackRO),
+      g_plans[plan] = {(int)z.n_rot, (int)total, (int)batch, (int)total_k, (int64_t)(lay.lin - kStackRO),
                        (int64_t)(lay.sched_o - kStackRO), (int64_t)(lay.sched_u - kStackRO)};
     else
       g_plans.erase(plan);

@@ -7,7 +7,9 @@ scripts/graph_decode_bench.py:70-118).  Two MI355X executors:
   * ``LinearStack`` -- every linear of the step in ONE persistent HIP launch
     (``tp_stack_run``); optional phase ordering makes a linear of phase p
     wait for all linears of phase p-1 (for a decoder layer: q/k/v, then o,
-    then gate/up, then down), as data dependencies would.
+    then gate/up, then down), the order data dependencies impose.  Ordering
+    schedules the work but passes no data: every input is rotated before any
+    phase runs, so one run cannot feed a phase's outputs to a later phase.
   * ``layer_forward`` -- one fused launch per group of linears sharing an
     input (q/k/v together, o, gate/up together, down): the launch structure a
     model with interleaved attention/norm kernels uses.
