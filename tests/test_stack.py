@@ -161,3 +161,66 @@ def test_headline_plan_matches_per_linear_and_oracle(cuda):
                 ref = O.tiled_forward(payload_numpy(p), x)
                 assert O.max_rel(stack.outputs[i].float().cpu().numpy(), ref) <= GEMV_TOL, (li, name)
         del stack
+
+
+def test_batch32_stack_mixed_blocks(cuda):
+    """192 linears at batch 32 (9216 rotation tiles, the wide kernel), with
+    Hadamard blocks 64..8192 (8192: two 4096-column sub-tiles summed) and
+    bias on every third.  Every output within 2e-3 of the per-linear forward
+    on the same input, and one linear of each shape within 2e-3 of the
+    oracle's tiled forward."""
+    from turbopress_amd.decode_step import LinearStack
+    from turbopress_amd.runtime import PackedTCQLinear
+    shapes = [(2560, 48), (576, 32), (8192, 32), (4096, 48), (9728, 32), (1024, 32)]  # (d, n)
+    payloads, entries = [], []
+    for g in range(32):
+        for j, (d, n) in enumerate(shapes):
+            p = make_payload(n, d, 3, 64, seed=5000 + 6 * g + j, bias=(g + j) % 3 == 0)
+            payloads.append(p)
+            x = make_activation(32, d, seed=7000 + 6 * g + j).to(cuda)
+            entries.append((PackedTCQLinear(p, mode="hip"), x, 0))
+    stack = LinearStack(entries)
+    for o in stack.outputs:
+        o.fill_(float("nan"))
+    stack.run()
+    torch.cuda.synchronize()
+    assert stack.error() == 0
+    for i, ((lin, x, _), y) in enumerate(zip(entries, stack.outputs)):
+        ref = lin(x).float()
+        err = float((y.float() - ref).abs().max() / ref.abs().max())
+        assert err <= GEMV_TOL, (i, shapes[i % 6], err)
+    for i in range(6):
+        ref = O.tiled_forward(payload_numpy(payloads[i]), entries[i][1].cpu().numpy())
+        assert O.max_rel(stack.outputs[i].float().cpu().numpy(), ref) <= GEMV_TOL, shapes[i]
+
+
+def test_stack_rotation_bit_exact(cuda):
+    """The rotation launch's z rows (the plan's last region, one [batch,
+    G4 * 256] fp16 block per linear in order) equal the oracle's
+    fp16(blockFWHT(x * rot_scale)) bit for bit, zero past d, for Hadamard
+    blocks 4..16384."""
+    from turbopress_amd.decode_step import LinearStack
+    from turbopress_amd.runtime import PackedTCQLinear
+    ds = [12, 40, 96, 128, 576, 1024, 2048, 2560, 3072, 4096, 6144, 8192, 9728, 16384]
+    batch = 3
+    payloads, entries = [], []
+    for i, d in enumerate(ds):
+        p = make_payload(16, d, 3, 64, seed=400 + i)
+        payloads.append(p)
+        gen = torch.Generator().manual_seed(500 + i)
+        x = (torch.randn(batch, d, generator=gen) * 3).to(torch.float16)
+        entries.append((PackedTCQLinear(p, mode="hip"), x.to(cuda), 0))
+    stack = LinearStack(entries)
+    stack.rotate()
+    torch.cuda.synchronize()
+    widths = [-(-d // 256) * 256 for d in ds]
+    zbytes = [batch * w * 2 for w in widths]
+    plan = stack.plan.cpu().numpy()
+    off = plan.size - sum(zbytes)
+    for p, (_, x, _), w, nb in zip(payloads, entries, widths, zbytes):
+        got = plan[off:off + nb].view(np.uint16).reshape(batch, w)
+        off += nb
+        d = int(p["d"])
+        ref = O.rotate_activations(payload_numpy(p), x.cpu().numpy()).astype(np.float16).view(np.uint16)
+        assert np.array_equal(got[:, :d], ref), (d, int(p["block"]))
+        assert not got[:, d:].any(), d

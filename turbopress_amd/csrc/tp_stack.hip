@@ -239,8 +239,8 @@ __device__ inline void wait_phase(const StackRO& P, uint32_t* pdone, StackCounte
 // 1024 and 2048 as one radix-4 step through LDS -- the stage order of the
 // reference's transform (distance 1, 2, 4, ... then one division by
 // sqrt(block)), all in fp32, z rounded to fp16 once.  A block larger than
-// 4096 (H_hb = H_(hb/4096) (x) H_4096) first sums its 4096-column sub-tiles
-// with the signs of the tile's row of H_(hb/4096).
+// 4096 (H_hb = H_(hb/4096) (x) H_4096) transforms each of its 4096-column
+// sub-tiles, then runs the stages across sub-tiles (4096, 8192) in order.
 
 constexpr int kRotTile = 4096;
 constexpr int kRotThreads = 256;
@@ -272,10 +272,137 @@ __device__ __forceinline__ void load16(__amdgpu_buffer_rsrc_t r, uint32_t off, f
   }
 }
 
+// v = x * rot_scale of 4096-column tile `k` of the item's row.
+__device__ __forceinline__ void rot_input(const TP_CONST RotItem& L, int k, int tid, float v[kRotEPT]) {
+  const uint32_t off = (uint32_t)(k * kRotTile + tid * kRotEPT) * 2u;
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(L.x, (uint32_t)L.d * 2u);
+  const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(L.rs, (uint32_t)L.d * 2u);
+  float rv[kRotEPT];
+  load16(xrs, off, v);
+  load16(rrs, off, rv);
+#pragma unroll
+  for (int e = 0; e < kRotEPT; ++e) v[e] *= rv[e];
+}
+
+// v / c, correctly rounded, for the fp32 c = sqrt(hb) of a power-of-two
+// block, from r = RN(1/c): q = RN(v r), then one correction step (Markstein:
+// e = v - q c is exact, RN(q + e r) is the rounded quotient).  Checked
+// against IEEE division for every fp32 v and every c = fp32(sqrt(2^j)),
+// j = 1..14: equal except where the quotient is an fp32 denormal (both round
+// to the same fp16 zero) and for v = -0 and +-inf, where q itself is the
+// answer (the correction would give +0 and NaN).
+__device__ __forceinline__ float div_by_block_root(float v, float c, float r) {
+  const float q = v * r;
+  const float e = __builtin_fmaf(-q, c, v);
+  const float q1 = __builtin_fmaf(e, r, q);
+  return __builtin_amdgcn_class(q, 0x264 /* -inf, -0, +0, +inf */) ? q : q1;
+}
+
+// Lane xor 1, 2, 4 or 8 (inside a row of 16 lanes) with DPP moves: no LDS.
+__device__ __forceinline__ float lane_xor_row(float v, int m) {
+  const int x = __builtin_bit_cast(int, v);
+  int y;
+  if (m == 1) {
+    y = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if (m == 2) {
+    y = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if (m == 4) {
+    // lanes 0-3 and 8-11 of a row read lane + 4 (row_shl:4), the others lane - 4 (row_shr:4)
+    y = __builtin_amdgcn_mov_dpp(x, 0x104, 0xF, 0x5, false);
+    y = __builtin_amdgcn_update_dpp(y, x, 0x114, 0xF, 0xA, false);
+  } else {
+    y = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);  // row_ror:8
+  }
+  return __builtin_bit_cast(float, y);
+}
+
+// Butterflies of a 4096-column tile at distances 1 .. hmax / 2 (hmax =
+// min(hb, 4096)), unnormalized.  `ex`: 4096 floats of LDS.  A butterfly's
+// two outputs a + b and a - b are one FMA each, fma(+-1, a, b): the product
+// is exact, so the sum rounds as the add or subtract does.
+__device__ __forceinline__ void rot_butterflies(float v[kRotEPT], int hmax, int tid, float* ex) {
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  // Stages are skipped with a (uniform) condition, never a loop exit: the
+  // loops must unroll so that every v[] index is a compile-time constant (a
+  // runtime stage distance would index the register array dynamically).
+#pragma unroll
+  for (int h = 1; h < kRotEPT; h <<= 1) {
+    if (h < hmax) {
+#pragma unroll
+      for (int e = 0; e < kRotEPT; ++e) {
+        if ((e & h) == 0) {
+          const float a = v[e], c = v[e + h];
+          v[e] = a + c;
+          v[e + h] = a - c;
+        }
+      }
+    }
+  }
+  // distances 16..512: lane bit sft; the upper lane of a pair keeps p - v
+#pragma unroll
+  for (int sft = 0; sft < 6; ++sft) {
+    if ((kRotEPT << sft) < hmax) {
+      const float sg = ((lane >> sft) & 1) ? -1.f : 1.f;
+#pragma unroll
+      for (int e = 0; e < kRotEPT; ++e) {
+        const float p = sft < 4 ? lane_xor_row(v[e], 1 << sft) : __shfl_xor(v[e], 1 << sft, 64);
+        v[e] = __builtin_fmaf(sg, v[e], p);
+      }
+    }
+  }
+  if (hmax > 1024) {  // distances 1024 (and 2048): wave bits of the column
+    __syncthreads();  // the previous item's reads of ex are done
+#pragma unroll
+    for (int e = 0; e < kRotEPT; ++e) ex[tid * kRotEPT + e] = v[e];
+    __syncthreads();
+    const int i0 = (lane * kRotEPT) & 1023;
+    const float s1 = (wave & 1) ? -1.f : 1.f;
+    if (hmax == 2048) {
+#pragma unroll
+      for (int e = 0; e < kRotEPT; ++e) {
+        const float p = ex[(wave ^ 1) * 1024 + i0 + e];
+        v[e] = __builtin_fmaf(s1, v[e], p);
+      }
+    } else {
+      const float s2 = (wave & 2) ? -1.f : 1.f;
+#pragma unroll
+      for (int e = 0; e < kRotEPT; ++e) {
+        const float u0 = ex[i0 + e], u1 = ex[1024 + i0 + e], u2 = ex[2048 + i0 + e], u3 = ex[3072 + i0 + e];
+        // natural-order H_4 row `wave`: stage 1024 then stage 2048
+        const float s01 = __builtin_fmaf(s1, u1, u0);
+        const float s23 = __builtin_fmaf(s1, u3, u2);
+        v[e] = __builtin_fmaf(s2, s23, s01);
+      }
+    }
+  }
+}
+
+// z = v / sqrt(hb) in fp16 into the item's z row (zero past d).
+__device__ __forceinline__ void rot_store(const TP_CONST RotItem& L, const float v[kRotEPT], int tid) {
+  const int c0 = L.k * kRotTile + tid * kRotEPT;
+  const int zld = L.zld;  // columns written (zero past d)
+  uint16_t* zr = L.z;
+  const float c = L.hdiv, r = 1.f / c;
+#pragma unroll
+  for (int g = 0; g < kRotEPT / 4; ++g) {
+    if (c0 + 4 * g >= zld) break;
+    float z4[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) z4[e] = div_by_block_root(v[4 * g + e], c, r);
+    const u32x2_t w = {(uint32_t)f2h(z4[0]) | ((uint32_t)f2h(z4[1]) << 16),
+                       (uint32_t)f2h(z4[2]) | ((uint32_t)f2h(z4[3]) << 16)};
+    *(TP_GLOBAL u32x2_t*)(zr + c0 + 4 * g) = w;
+  }
+}
+
 // One workgroup per tile when the host knows the tile count (ONE_TILE: the
 // descriptor is the first load, the x / rot_scale loads the second);
-// otherwise a grid-stride loop bounded by the plan's count.
-template <bool ONE_TILE>
+// otherwise a grid-stride loop bounded by the plan's count.  BIG selects the
+// tiles of blocks above 4096 columns (their registers would halve the
+// occupancy of the common case), !BIG the others; a plan with big blocks
+// gets both launches.
+template <bool ONE_TILE, bool BIG>
 __global__ void __launch_bounds__(kRotThreads)
 tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
   __shared__ float ex[kRotTile];
@@ -284,98 +411,44 @@ tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
   const int step = ONE_TILE ? 1 : (int)gridDim.x;
   const RotItem* items = reinterpret_cast<const RotItem*>(plan_ro + (kRotItems - kStackRO));
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
   for (int item = first; item < end; item += step) {
     const TP_CONST RotItem& L = cread(items + item);
-    const int k = L.k;
-    const int c0 = k * kRotTile + tid * kRotEPT;      // first column of this thread
-    const int hb = L.hb;
-    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(L.x, (uint32_t)L.d * 2u);
-    const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(L.rs, (uint32_t)L.d * 2u);
+    if ((L.hb > kRotTile) != BIG) continue;  // (uniform)
     float v[kRotEPT];
-    if (hb <= kRotTile) {
-      float rv[kRotEPT];
-      load16(xrs, (uint32_t)c0 * 2u, v);
-      load16(rrs, (uint32_t)c0 * 2u, rv);
-#pragma unroll
-      for (int e = 0; e < kRotEPT; ++e) v[e] *= rv[e];
+    if (!BIG) {
+      rot_input(L, L.k, tid, v);
+      rot_butterflies(v, L.hb, tid, ex);
     } else {
-      const int cb = k * kRotTile;
-      const int base = cb - cb % hb, o = (cb % hb) / kRotTile;
+      // H_hb = H_(hb/4096) (x) H_4096, stages in order of distance: every
+      // 4096-column sub-tile of the block through distances 1..2048, then
+      // distance 4096 (sub-tile pairs) and 8192 (pairs of pairs); sub-tile o
+      // of the result takes the signs of row o.
+      const int nsub = L.hb / kRotTile;        // 2 or 4
+      const int o = L.k % nsub, k0 = L.k - o;  // this tile's sub-tile, the block's first
+      const float s1 = (o & 1) ? -1.f : 1.f, s2 = (o & 2) ? -1.f : 1.f;
+      float a[kRotEPT];
+#pragma unroll 1
+      for (int i = 0; i < nsub; ++i) {
+        float t[kRotEPT];
+        rot_input(L, k0 + i, tid, t);
+        rot_butterflies(t, kRotTile, tid, ex);
+        if ((i & 1) == 0) {
 #pragma unroll
-      for (int e = 0; e < kRotEPT; ++e) v[e] = 0.f;
-      for (int i = 0; i < hb / kRotTile; ++i) {
-        const int c = base + i * kRotTile + tid * kRotEPT;
-        float xv[kRotEPT], rv[kRotEPT];
-        load16(xrs, (uint32_t)c * 2u, xv);
-        load16(rrs, (uint32_t)c * 2u, rv);
-        const bool neg = __popc(i & o) & 1;
+          for (int e = 0; e < kRotEPT; ++e) a[e] = t[e];
+        } else {
 #pragma unroll
-        for (int e = 0; e < kRotEPT; ++e) v[e] += neg ? -(xv[e] * rv[e]) : xv[e] * rv[e];
-      }
-    }
-    const int hmax = hb < kRotTile ? hb : kRotTile;
-    // Stages are skipped with a (uniform) condition, never a loop exit: the
-    // loops must unroll so that every v[] index is a compile-time constant (a
-    // runtime stage distance would index the register array dynamically).
+          for (int e = 0; e < kRotEPT; ++e) a[e] = __builtin_fmaf(s1, t[e], a[e]);  // distance 4096
+          if (i == 1) {
 #pragma unroll
-    for (int h = 1; h < kRotEPT; h <<= 1) {
-      if (h < hmax) {
+            for (int e = 0; e < kRotEPT; ++e) v[e] = a[e];
+          } else {
 #pragma unroll
-        for (int e = 0; e < kRotEPT; ++e) {
-          if ((e & h) == 0) {
-            const float a = v[e], c = v[e + h];
-            v[e] = a + c;
-            v[e + h] = a - c;
+            for (int e = 0; e < kRotEPT; ++e) v[e] = __builtin_fmaf(s2, a[e], v[e]);  // distance 8192
           }
         }
       }
     }
-#pragma unroll
-    for (int sft = 0; sft < 6; ++sft) {
-      if ((kRotEPT << sft) < hmax) {
-        const bool upper = (lane >> sft) & 1;
-#pragma unroll
-        for (int e = 0; e < kRotEPT; ++e) {
-          const float p = __shfl_xor(v[e], 1 << sft, 64);
-          v[e] = upper ? p - v[e] : v[e] + p;
-        }
-      }
-    }
-    if (hmax > 1024) {  // distances 1024 (and 2048): wave bits of the column
-      __syncthreads();  // the previous item's reads of ex are done
-#pragma unroll
-      for (int e = 0; e < kRotEPT; ++e) ex[tid * kRotEPT + e] = v[e];
-      __syncthreads();
-      const int i0 = (lane * kRotEPT) & 1023;
-      if (hmax == 2048) {
-        const int w2 = wave & 1;
-#pragma unroll
-        for (int e = 0; e < kRotEPT; ++e) {
-          const float p = ex[(wave ^ 1) * 1024 + i0 + e];
-          v[e] = w2 ? p - v[e] : v[e] + p;
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < kRotEPT; ++e) {
-          const float u0 = ex[i0 + e], u1 = ex[1024 + i0 + e], u2 = ex[2048 + i0 + e], u3 = ex[3072 + i0 + e];
-          // natural-order H_4 row `wave`: stage 1024 then stage 2048
-          const float s01 = (wave & 1) ? u0 - u1 : u0 + u1;
-          const float s23 = (wave & 1) ? u2 - u3 : u2 + u3;
-          v[e] = (wave & 2) ? s01 - s23 : s01 + s23;
-        }
-      }
-    }
-    const int zld = L.zld;                           // columns written (zero past d)
-    uint16_t* zr = L.z;
-#pragma unroll
-    for (int g = 0; g < kRotEPT / 4; ++g) {
-      if (c0 + 4 * g >= zld) break;
-      const u32x2_t w = {(uint32_t)f2h(v[4 * g] / L.hdiv) | ((uint32_t)f2h(v[4 * g + 1] / L.hdiv) << 16),
-                         (uint32_t)f2h(v[4 * g + 2] / L.hdiv) | ((uint32_t)f2h(v[4 * g + 3] / L.hdiv) << 16)};
-      *(TP_GLOBAL u32x2_t*)(zr + c0 + 4 * g) = w;
-    }
+    rot_store(L, v, tid);
   }
 }
 
@@ -1524,6 +1597,7 @@ int linear_forward_wide(const LinearDesc& Lin, const uint16_t* z, int64_t zld, i
 // did not initialise gets kernels that read these from the plan header.
 struct PlanReg {
   int n_rot, total, batch, total_k;
+  bool big_rot;  // some linear has a Hadamard block above 4096 columns
   int64_t lin_off, sched_o_off, sched_u_off;
 };
 std::mutex g_plan_mutex;
@@ -1645,6 +1719,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
   int32_t* ptiles = reinterpret_cast<int32_t*>(host + lay.ptiles);
   OrdBlockDesc* oblk = reinterpret_cast<OrdBlockDesc*>(host + lay.oblk);
   int64_t total_k = 0;
+  bool big_rot = false;
   RotItem* items = reinterpret_cast<RotItem*>(host + lay.rot_items);
   char* zbuf = reinterpret_cast<char*>(plan) + lay.zbuf;
   int64_t total = 0, rot = 0, zoff = 0;
@@ -1658,6 +1733,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     }
     const int64_t hb = l.block;
     if (hb < 1 || (hb & (hb - 1)) || l.d % hb || hb > 16384) { st = TP_ERR_BAD_BLOCK; break; }
+    if (hb > kRotTile) big_rot = true;
     if (l.ldx < l.d || (l.ldx & 3) || (l.d & 3) || ((uintptr_t)l.x & 7) || ((uintptr_t)l.rot_scale & 7) ||
         ((uintptr_t)l.path_tiled & 15) || ((uintptr_t)l.member_tiled & 15)) {
       st = TP_ERR_MISALIGNED;
@@ -1751,7 +1827,7 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
   {
     std::lock_guard<std::mutex> lock(g_plan_mutex);
     if (st == TP_OK && z.n_rot > 0)
-      g_plans[plan] = {(int)z.n_rot, (int)total, (int)batch, (int)total_k, (int64_t)(lay.lin - kStackRO),
+      g_plans[plan] = {(int)z.n_rot, (int)total, (int)batch, (int)total_k, big_rot, (int64_t)(lay.lin - kStackRO),
                        (int64_t)(lay.sched_o - kStackRO), (int64_t)(lay.sched_u - kStackRO)};
     else
       g_plans.erase(plan);
@@ -1765,12 +1841,20 @@ extern "C" int tp_stack_rotate(void* plan, int64_t batch, void* stream) {
   if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
   const char* ro = reinterpret_cast<const char*>(plan) + kStackRO;
   PlanReg reg;
-  const int n_rot = plan_lookup(plan, &reg) ? reg.n_rot : 0;
-  if (n_rot > 0)
-    hipLaunchKernelGGL(tcq_stack_rotate_kernel<true>, dim3(n_rot), dim3(kRotThreads), 0, (hipStream_t)stream, ro);
-  else
-    hipLaunchKernelGGL(tcq_stack_rotate_kernel<false>, dim3(2 * device_cu_count()), dim3(kRotThreads), 0,
+  const bool known = plan_lookup(plan, &reg);
+  const int n_rot = known ? reg.n_rot : 0;
+  if (n_rot > 0) {
+    hipLaunchKernelGGL((tcq_stack_rotate_kernel<true, false>), dim3(n_rot), dim3(kRotThreads), 0,
                        (hipStream_t)stream, ro);
+    if (reg.big_rot)
+      hipLaunchKernelGGL((tcq_stack_rotate_kernel<true, true>), dim3(n_rot), dim3(kRotThreads), 0,
+                         (hipStream_t)stream, ro);
+  } else {
+    hipLaunchKernelGGL((tcq_stack_rotate_kernel<false, false>), dim3(2 * device_cu_count()), dim3(kRotThreads), 0,
+                       (hipStream_t)stream, ro);
+    hipLaunchKernelGGL((tcq_stack_rotate_kernel<false, true>), dim3(2 * device_cu_count()), dim3(kRotThreads), 0,
+                       (hipStream_t)stream, ro);
+  }
   return launch_status();
 }
 
