@@ -288,9 +288,10 @@ __device__ __forceinline__ void rot_input(const TP_CONST RotItem& L, int k, int 
 // block, from r = RN(1/c): q = RN(v r), then one correction step (Markstein:
 // e = v - q c is exact, RN(q + e r) is the rounded quotient).  Checked
 // against IEEE division for every fp32 v and every c = fp32(sqrt(2^j)),
-// j = 1..14: equal except where the quotient is an fp32 denormal (both round
-// to the same fp16 zero) and for v = -0 and +-inf, where q itself is the
-// answer (the correction would give +0 and NaN).
+// j = 1..14: equal wherever |v / c| >= 2^-105 (below, the residual
+// underflows, and both quotients round to the same fp16 signed zero), given
+// that for v = -0 and +-inf q itself is the answer (the correction would
+// give +0 and NaN).
 __device__ __forceinline__ float div_by_block_root(float v, float c, float r) {
   const float q = v * r;
   const float e = __builtin_fmaf(-q, c, v);
