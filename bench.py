@@ -259,9 +259,10 @@ def copy_reference(mib: int, reps: int = 10):
 
 
 def read_reference(nbytes: int, reps: int = 20, settle_ms: float = 0.0):
-    """A plain streaming read (tp_read_probe: grid-stride 16-byte loads, no
-    compute) of as many bytes as one step moves: the read bandwidth this box
-    reaches at all, i.e. the practical ceiling of an HBM-bound read stream."""
+    """A plain streaming read (tp_read_probe: every wave streams its own
+    contiguous slice with 16-byte loads, no compute) of as many bytes as one
+    step moves: the read bandwidth this box reaches at all, i.e. the
+    practical ceiling of an HBM-bound read stream."""
     from turbopress_amd import _lib
     lib = _lib.lib()
     nbytes = (nbytes + 15) & ~15

@@ -43,9 +43,10 @@ int tp_abi_version(void);
 const char* tp_status_string(int status);
 
 /* Read `bytes` (a multiple of 16, 16-byte aligned) of device memory once
- * with a plain streaming-read kernel (grid-stride 16-byte loads, 4
- * workgroups per CU); `sink` (one device word) is written only in the
- * practically impossible case that the XOR of all words hits a constant.
+ * with a plain streaming-read kernel (each wave streams a contiguous slice
+ * with 16-byte loads, 2 workgroups of 8 waves per CU); `sink` (one device
+ * word) is written only in the practically impossible case that the XOR of
+ * all words hits a constant.
  * Benchmark utility: the achievable read bandwidth of the GPU it runs on,
  * the practical ceiling of an HBM-bound read stream.  No reference
  * counterpart. */

@@ -37,24 +37,32 @@ extern "C" int tp_subset_lut(int n_states, uint8_t* lut_out, int lut_len) {
   return TP_OK;
 }
 
-// Streaming read of `n16` 16-byte words: grid-stride, eight loads in flight
-// per thread, XOR-folded so that nothing is elided; one word is stored only
-// when the fold hits an arbitrary constant (practically never).
+// Streaming read of `n16` 16-byte words.  Every wave streams its own
+// contiguous slice (a multiple of 64 words), eight 1 KiB loads in flight:
+// on MI355X this reads ~12 % faster than a grid-stride sweep of the same
+// bytes (whose loads all land in one sliding window of the address space).
+// XOR-folded so that nothing is elided; one word is stored only when the
+// fold hits an arbitrary constant (practically never).
 typedef uint32_t probe_v4 __attribute__((ext_vector_type(4)));
 __global__ void __launch_bounds__(512) tp_read_probe_kernel(const probe_v4* __restrict__ p, uint64_t n16,
                                                             uint32_t* __restrict__ sink) {
   constexpr int U = 8;
-  const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
-  uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const uint64_t waves = (uint64_t)gridDim.x * (blockDim.x >> 6);
+  const uint64_t w = (uint64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const uint64_t per = ((n16 + waves - 1) / waves + 63) & ~(uint64_t)63;
+  const uint64_t lo = w * per;
+  const uint64_t hi = lo + per < n16 ? lo + per : n16;
   probe_v4 acc = {0u, 0u, 0u, 0u};
-  for (; i + (U - 1) * stride < n16; i += U * stride) {
+  uint64_t i = lo;
+  for (; i + 64 * U <= hi; i += 64 * U) {
     probe_v4 v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(p + i + u * stride);
+    for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(p + i + 64 * u + lane);
 #pragma unroll
     for (int u = 0; u < U; ++u) acc ^= v[u];
   }
-  for (; i < n16; i += stride) acc ^= p[i];
+  for (i += lane; i < hi; i += 64) acc ^= p[i];
   if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9E3779B9u) sink[0] = 1u;
 }
 
@@ -62,7 +70,7 @@ extern "C" int tp_read_probe(const void* buf, int64_t bytes, uint32_t* sink, voi
   if (!buf || !sink) return TP_ERR_NULL_POINTER;
   if (bytes < 16 || (bytes & 15)) return TP_ERR_BAD_DIMS;
   if ((uintptr_t)buf & 15) return TP_ERR_MISALIGNED;
-  const int grid = 4 * tp::device_cu_count();  // 4 workgroups of 512 threads per CU
+  const int grid = 2 * tp::device_cu_count();  // 2 workgroups of 512 threads per CU
   hipLaunchKernelGGL(tp_read_probe_kernel, dim3(grid), dim3(512), 0, (hipStream_t)stream,
                      reinterpret_cast<const probe_v4*>(buf), (uint64_t)bytes / 16u, sink);
   return tp::launch_status();
