@@ -38,7 +38,8 @@ extern "C" int tp_subset_lut(int n_states, uint8_t* lut_out, int lut_len) {
 }
 
 // Streaming read of `n16` 16-byte words.  Every wave streams its own
-// contiguous slice (a multiple of 64 words), eight 1 KiB loads in flight:
+// contiguous slice (a multiple of 64 words), eight 1 KiB loads in flight
+// (short slices too: the loads past the slice are masked off):
 // on MI355X this reads ~12 % faster than a grid-stride sweep of the same
 // bytes (whose loads all land in one sliding window of the address space).
 // XOR-folded so that nothing is elided; one word is stored only when the
@@ -54,15 +55,16 @@ __global__ void __launch_bounds__(512) tp_read_probe_kernel(const probe_v4* __re
   const uint64_t lo = w * per;
   const uint64_t hi = lo + per < n16 ? lo + per : n16;
   probe_v4 acc = {0u, 0u, 0u, 0u};
-  uint64_t i = lo;
-  for (; i + 64 * U <= hi; i += 64 * U) {
+  for (uint64_t i = lo; i < hi; i += 64 * U) {
     probe_v4 v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(p + i + 64 * u + lane);
+    for (int u = 0; u < U; ++u) {
+      const uint64_t k = i + 64 * u + lane;
+      v[u] = k < hi ? __builtin_nontemporal_load(p + k) : probe_v4{0u, 0u, 0u, 0u};
+    }
 #pragma unroll
     for (int u = 0; u < U; ++u) acc ^= v[u];
   }
-  for (i += lane; i < hi; i += 64) acc ^= p[i];
   if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9E3779B9u) sink[0] = 1u;
 }
 
