@@ -156,7 +156,7 @@ int tp_retile(const uint8_t* path, int64_t path_stride, const uint8_t* member,
               uint8_t* path_tiled, uint8_t* member_tiled, void* stream);
 
 /* Bytes of split-K workspace tp_tcq_gemv_tiled needs for n rows at `batch`
- * (0 for invalid sizes).  The workspace must be zero before the first call;
+ * (0 for invalid sizes: n outside [1, 2^30], batch outside [1, 32]).  The workspace must be zero before the first call;
  * every call leaves it zero again, so one allocation serves any number of
  * calls (and graph replays) on one stream. */
 int64_t tp_gemv_workspace_bytes(int64_t n, int64_t batch);

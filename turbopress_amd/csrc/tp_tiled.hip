@@ -388,7 +388,8 @@ extern "C" int tp_retile(const uint8_t* path, int64_t path_stride, const uint8_t
 }
 
 extern "C" int64_t tp_gemv_workspace_bytes(int64_t n, int64_t batch) {
-  if (n <= 0 || batch <= 0) return 0;
+  // (the tiled layout holds at most 2^26 row tiles)
+  if (n <= 0 || n > ((int64_t)1 << 30) || batch <= 0 || batch > 32) return 0;
   const int64_t T = (n + kTileRows - 1) / kTileRows;
   const int64_t nbt = batch <= 16 ? 1 : 2;
   return T * kTileRows * 16 * nbt * 4 + T * 4;

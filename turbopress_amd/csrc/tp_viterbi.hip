@@ -208,7 +208,7 @@ int launch_viterbi(int bits, const float* z, int64_t ldz, int64_t n, int d, cons
 using namespace tp;
 
 extern "C" int64_t tp_viterbi_workspace_bytes(int64_t n, int64_t d) {
-  if (n <= 0 || d <= 0) return 0;
+  if (n <= 0 || d <= 0 || n > INT64_MAX / (int64_t)sizeof(uint64_t) / d) return 0;
   return n * d * (int64_t)sizeof(uint64_t);
 }
 
