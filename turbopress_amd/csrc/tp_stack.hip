@@ -856,6 +856,34 @@ __device__ inline void count_phase_tiles(uint32_t* odone, int ph, uint32_t tiles
     __hip_atomic_fetch_add(ctr + r * kOrdLineWords, tiles, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// y[row0 .. row0+3] of one batch row = fp16(v * scale) (+ bias) for the rows
+// below n (sc: the four rows' fp16 scales).  When all four rows exist and y
+// is 8-byte aligned, one 8-byte store (and one 8-byte bias load) instead of
+// four 2-byte ones.
+__device__ __forceinline__ void store_rows4(uint16_t* yr, const uint16_t* bias, int row0, int n, const float v[4],
+                                            u32x2_t sc) {
+  uint16_t out[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) out[j] = f2h(v[j] * h2f((uint16_t)(sc[j >> 1] >> (16 * (j & 1)))));
+  if (row0 + 4 <= n && ((reinterpret_cast<uintptr_t>(yr + row0) | reinterpret_cast<uintptr_t>(bias + row0)) & 7) == 0) {
+    if (bias) {
+      const u32x2_t bw = *(const TP_GLOBAL u32x2_t*)(bias + row0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out[j] = f2h(h2f(out[j]) + h2f((uint16_t)(bw[j >> 1] >> (16 * (j & 1)))));
+    }
+    const u32x2_t w = {(uint32_t)out[0] | ((uint32_t)out[1] << 16), (uint32_t)out[2] | ((uint32_t)out[3] << 16)};
+    *(TP_GLOBAL u32x2_t*)(yr + row0) = w;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (row0 + j >= n) continue;
+      uint16_t o = out[j];
+      if (bias) o = f2h(h2f(o) + h2f(gld(bias + row0 + j)));
+      gst(yr + row0 + j, o);
+    }
+  }
+}
+
 // Where one block of the ordered schedule sits, and the wave's chunk of it
 // (scalar values, read one block ahead).
 struct OrdDesc {
@@ -1100,15 +1128,8 @@ tcq_stack_ordered_kernel(const char* __restrict__ plan_ro, char* __restrict__ pl
           }
         }
         if (bb < batch) {
-          const int row0 = (D.t0 + t) * kTileRows + 4 * q;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int row = row0 + j;
-            if (row >= D.n) continue;
-            uint16_t out = f2h(v[j] * h2f((uint16_t)(B.sc[i][j >> 1] >> (16 * (j & 1)))));
-            if (D.bias) out = f2h(h2f(out) + h2f(gld(D.bias + row)));
-            gst(D.y + (size_t)bb * D.ldy + row, out);
-          }
+          const float vv[4] = {v[0], v[1], v[2], v[3]};
+          store_rows4(D.y + (size_t)bb * D.ldy, D.bias, (D.t0 + t) * kTileRows + 4 * q, D.n, vv, B.sc[i]);
         }
       }
     }
