@@ -1,6 +1,7 @@
 """The stack rotation divides by sqrt(block) with a corrected reciprocal
-product instead of an IEEE division (turbopress_amd/csrc/tp_stack.hip,
-div_by_block_root).  Restated here in C (fmaf) and checked against IEEE
+product instead of an IEEE division (div_by_block_root in
+turbopress_amd/csrc/tp_tiled_common.h; the stack rotation and the rotations
+inside the per-linear launches).  Restated here in C (fmaf) and checked against IEEE
 division for every Hadamard block 2..16384 on a strided sample of all fp32
 bit patterns plus the special values: the quotients are equal wherever
 |v / c| >= 2^-100; below that the residual underflows, and both quotients

@@ -65,19 +65,21 @@ __device__ __forceinline__ void lin_chunk_fwht(const LinArgs& a, int lane, float
     p = v[1]; q = v[3];
     v[1] = p + q; v[3] = p - q;
   }
+  // (the upper lane of a pair keeps p - v: one FMA with the lane's sign)
 #pragma unroll
   for (int sft = 0; sft < 6; ++sft) {
     if ((4 << sft) < hmax) {
-      const bool upper = (lane >> sft) & 1;
+      const float sg = ((lane >> sft) & 1) ? -1.f : 1.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float p = __shfl_xor(v[e], 1 << sft, 64);
-        v[e] = upper ? p - v[e] : v[e] + p;
+        const float p = sft < 4 ? lane_xor_row(v[e], 1 << sft) : __shfl_xor(v[e], 1 << sft, 64);
+        v[e] = __builtin_fmaf(sg, v[e], p);
       }
     }
   }
+  const float r = 1.f / a.hdiv;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = v[e] / a.hdiv;
+  for (int e = 0; e < 4; ++e) v[e] = div_by_block_root(v[e], a.hdiv, r);
 }
 
 // z of one 256-column chunk of batch row b for Hadamard blocks <= 512, four

@@ -284,39 +284,6 @@ __device__ __forceinline__ void rot_input(const TP_CONST RotItem& L, int k, int 
   for (int e = 0; e < kRotEPT; ++e) v[e] *= rv[e];
 }
 
-// v / c, correctly rounded, for the fp32 c = sqrt(hb) of a power-of-two
-// block, from r = RN(1/c): q = RN(v r), then one correction step (Markstein:
-// e = v - q c is exact, RN(q + e r) is the rounded quotient).  Checked
-// against IEEE division for every fp32 v and every c = fp32(sqrt(2^j)),
-// j = 1..14: equal wherever |v / c| >= 2^-105 (below, the residual
-// underflows, and both quotients round to the same fp16 signed zero), given
-// that for v = -0 and +-inf q itself is the answer (the correction would
-// give +0 and NaN).
-__device__ __forceinline__ float div_by_block_root(float v, float c, float r) {
-  const float q = v * r;
-  const float e = __builtin_fmaf(-q, c, v);
-  const float q1 = __builtin_fmaf(e, r, q);
-  return __builtin_amdgcn_class(q, 0x264 /* -inf, -0, +0, +inf */) ? q : q1;
-}
-
-// Lane xor 1, 2, 4 or 8 (inside a row of 16 lanes) with DPP moves: no LDS.
-__device__ __forceinline__ float lane_xor_row(float v, int m) {
-  const int x = __builtin_bit_cast(int, v);
-  int y;
-  if (m == 1) {
-    y = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
-  } else if (m == 2) {
-    y = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
-  } else if (m == 4) {
-    // lanes 0-3 and 8-11 of a row read lane + 4 (row_shl:4), the others lane - 4 (row_shr:4)
-    y = __builtin_amdgcn_mov_dpp(x, 0x104, 0xF, 0x5, false);
-    y = __builtin_amdgcn_update_dpp(y, x, 0x114, 0xF, 0xA, false);
-  } else {
-    y = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);  // row_ror:8
-  }
-  return __builtin_bit_cast(float, y);
-}
-
 // Butterflies of a 4096-column tile at distances 1 .. hmax / 2 (hmax =
 // min(hb, 4096)), unnormalized.  `ex`: 4096 floats of LDS.  A butterfly's
 // two outputs a + b and a - b are one FMA each, fma(+-1, a, b): the product
@@ -1276,6 +1243,7 @@ __device__ __forceinline__ XChunk wide_load_x(const LinearDesc& L, int batch, in
 // reference's transform, all in fp32, one rounding to fp16.
 __device__ __forceinline__ ZChunk wide_rotate(const XChunk& c, int lane, int hb, float hdiv) {
   ZChunk z;
+  const float rdiv = 1.f / hdiv;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     float v[8];
@@ -1298,20 +1266,22 @@ __device__ __forceinline__ ZChunk wide_rotate(const XChunk& c, int lane, int hb,
         }
       }
     }
+    // (the upper lane of a pair keeps p - v: one FMA with the lane's sign)
 #pragma unroll
     for (int sft = 0; sft < 6; ++sft) {
       if ((8 << sft) < hb) {
-        const bool upper = (lane >> sft) & 1;
+        const float sg = ((lane >> sft) & 1) ? -1.f : 1.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float p = __shfl_xor(v[e], 1 << sft, 64);
-          v[e] = upper ? p - v[e] : v[e] + p;
+          const float p = sft < 4 ? lane_xor_row(v[e], 1 << sft) : __shfl_xor(v[e], 1 << sft, 64);
+          v[e] = __builtin_fmaf(sg, v[e], p);
         }
       }
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      z.v[k][e] = (uint32_t)f2h(v[2 * e] / hdiv) | ((uint32_t)f2h(v[2 * e + 1] / hdiv) << 16);
+      z.v[k][e] = (uint32_t)f2h(div_by_block_root(v[2 * e], hdiv, rdiv)) |
+                  ((uint32_t)f2h(div_by_block_root(v[2 * e + 1], hdiv, rdiv)) << 16);
   }
   return z;
 }
@@ -1373,6 +1343,13 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
   for (int bt = 0; bt < NBT; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
   // halo of the range's first unit: word 1 of the previous unit's last segment
   uint32_t x1_last = ch0 > 0 ? pt[((4 * ch0 * kMaxUnitsPerBlock - 1) * kTileRows + r) * 2 + 1] : 0u;
+  // the epilogue's row scales and bias (rows 4q..4q+3 of the tile, zeros
+  // past n), loaded now so that they are in registers when the sums are
+  const int row0 = t * kTileRows + 4 * q;
+  const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(L.scales, (uint32_t)L.n * 2u);
+  const __amdgpu_buffer_rsrc_t brs = buffer_rsrc(L.bias, L.bias ? (uint32_t)L.n * 2u : 0u);
+  const u32x2_t sc4 = __builtin_amdgcn_raw_buffer_load_b64(srs, active ? (uint32_t)row0 * 2u : kOutOfRange, 0, 0);
+  const u32x2_t bs4 = __builtin_amdgcn_raw_buffer_load_b64(brs, active ? (uint32_t)row0 * 2u : kOutOfRange, 0, 0);
   // The first chunk's z, then its weights: the z staging waits for the z
   // loads only, and the weights are in flight during it (and during the
   // table build).
@@ -1426,7 +1403,6 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
   if (!active) return;
 
   // Epilogue: lane holds rows 4q..4q+3 of its tile for batch column r.
-  const int row0 = t * kTileRows + 4 * q;
   float v[NBT][4];
 #pragma unroll
   for (int bt = 0; bt < NBT; ++bt)
@@ -1458,8 +1434,8 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
   for (int i = 0; i < 4; ++i) {
     const int row = row0 + i;
     if (row >= L.n) continue;
-    const float sc = h2f(gld(L.scales + row));
-    const float bs = L.bias ? h2f(gld(L.bias + row)) : 0.f;
+    const float sc = h2f((uint16_t)(sc4[i >> 1] >> (16 * (i & 1))));
+    const float bs = h2f((uint16_t)(bs4[i >> 1] >> (16 * (i & 1))));
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt) {
       const int nb = bt * 16 + r;

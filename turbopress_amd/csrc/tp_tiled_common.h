@@ -59,6 +59,39 @@ __host__ __device__ constexpr int member_words(int bits) {
   return bits == 2 ? 2 : bits == 3 ? 4 : bits == 4 ? 6 : 0;
 }
 
+// v / c, correctly rounded, for the fp32 c = sqrt(hb) of a power-of-two
+// block, from r = RN(1/c): q = RN(v r), then one correction step (Markstein:
+// e = v - q c is exact, RN(q + e r) is the rounded quotient).  Checked
+// against IEEE division for every fp32 v and every c = fp32(sqrt(2^j)),
+// j = 1..14: equal wherever |v / c| >= 2^-105 (below, the residual
+// underflows, and both quotients round to the same fp16 signed zero), given
+// that for v = -0 and +-inf q itself is the answer (the correction would
+// give +0 and NaN).
+__device__ __forceinline__ float div_by_block_root(float v, float c, float r) {
+  const float q = v * r;
+  const float e = __builtin_fmaf(-q, c, v);
+  const float q1 = __builtin_fmaf(e, r, q);
+  return __builtin_amdgcn_class(q, 0x264 /* -inf, -0, +0, +inf */) ? q : q1;
+}
+
+// Lane xor 1, 2, 4 or 8 (inside a row of 16 lanes) with DPP moves: no LDS.
+__device__ __forceinline__ float lane_xor_row(float v, int m) {
+  const int x = __builtin_bit_cast(int, v);
+  int y;
+  if (m == 1) {
+    y = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  } else if (m == 2) {
+    y = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else if (m == 4) {
+    // lanes 0-3 and 8-11 of a row read lane + 4 (row_shl:4), the others lane - 4 (row_shr:4)
+    y = __builtin_amdgcn_mov_dpp(x, 0x104, 0xF, 0x5, false);
+    y = __builtin_amdgcn_update_dpp(y, x, 0x114, 0xF, 0xA, false);
+  } else {
+    y = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);  // row_ror:8
+  }
+  return __builtin_bit_cast(float, y);
+}
+
 // Delay mask of a window-coordinate generator: bit t set when the subset bit
 // XORs in the path bit t columns back.
 __host__ __device__ constexpr uint32_t delay_mask(uint32_t g, int m) {
