@@ -20,6 +20,10 @@ _LAZY = {
     "subset_lut": ("turbopress_amd.hip_kernel", "subset_lut"),
     "window_decode_levels": ("turbopress_amd.hip_kernel", "window_decode_levels"),
     "default_codebook": ("turbopress_amd.codebooks", "default_codebook"),
+    "pack_linear": ("turbopress_amd.pack", "pack_linear"),
+    "pack_model": ("turbopress_amd.pack", "pack_model"),
+    "load_packed_model": ("turbopress_amd.artifact", "load_packed_model"),
+    "tcq_quantize_rows": ("turbopress_amd.encoder", "tcq_quantize_rows"),
 }
 
 __all__ = list(_LAZY)

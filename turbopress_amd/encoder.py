@@ -82,11 +82,17 @@ class TCQQuantized:
 
 def tcq_quantize_rows(w: Tensor, bits: int, n_states: int = 8, scale_iters: int = 1,
                       codebook: Tensor | None = None) -> TCQQuantized:
-    """TCQ-quantize each row of ``w`` [n_rows, dim] at ``bits`` bits/weight on
-    the GPU (trellis.py:256-320): per-row RMS scale, Viterbi on w/scale, then
+    """TCQ-quantize each row of ``w`` [n_rows, dim] at ``bits`` bits/weight
+    (trellis.py:256-320): per-row RMS scale, Viterbi on w/scale, then
     ``scale_iters`` least-squares scale refits each followed by a new search.
     Zero rows get scale 0.  ``codebook`` (fp32 [2^(bits+1)]) defaults to the
-    stored trellis-optimised codebook for (bits, n_states) when one exists."""
+    trellis-optimised codebook for (bits, n_states), the reference's default
+    (``codebook_mode="optimized"``).
+
+    The row statistics and refits run on ``w``'s device with the reference's
+    torch ops (so a CPU ``w``, as ``pack_linear`` passes, gives the
+    reference's scales bit for bit); only the Viterbi searches run on the
+    GPU (``tp_tcq_viterbi``).  The results are on ``w``'s device."""
     if w.ndim != 2:
         raise ValueError(f"expected a 2D tensor [n_rows, dim], got shape {tuple(w.shape)}")
     if not torch.is_floating_point(w):
@@ -96,23 +102,29 @@ def tcq_quantize_rows(w: Tensor, bits: int, n_states: int = 8, scale_iters: int 
     if scale_iters < 0:
         raise ValueError(f"scale_iters must be >= 0, got {scale_iters}")
     if codebook is None:
-        from turbopress_amd.codebooks import available_codebooks, default_codebook
+        from turbopress_amd.codebooks import available_codebooks, optimized_codebook_f32
         if (bits, n_states) not in available_codebooks():
             raise ValueError(f"no stored codebook for bits={bits}, n_states={n_states}: pass one")
-        codebook = default_codebook(bits, n_states)
-    dev = w.device if w.is_cuda else torch.device("cuda", torch.cuda.current_device())
-    w32 = w.to(device=dev, dtype=torch.float32)
-    cb = codebook.to(device=dev, dtype=torch.float32)
+        codebook = optimized_codebook_f32(bits, n_states)
+    gpu = w.device if w.is_cuda else torch.device("cuda", torch.cuda.current_device())
+    w32 = w.to(torch.float32)
+    cb = codebook.to(device=w32.device, dtype=torch.float32)
+    cb_gpu = cb.to(gpu)
+
+    def search(z: Tensor):
+        level, path, member, _ = viterbi(z.to(gpu), cb_gpu, n_states)
+        return level.to(w32.device), path.to(w32.device), member.to(w32.device)
+
     scales = w32.pow(2).mean(dim=1).sqrt()
     nonzero = scales > 0
     safe = torch.where(nonzero, scales, torch.ones_like(scales))
-    level, path, member, _ = viterbi(w32 / safe[:, None], cb, n_states)
+    level, path, member = search(w32 / safe[:, None])
     for _ in range(scale_iters):
         q = cb[level.long()]
         num = (w32 * q).sum(dim=1)
         den = (q * q).sum(dim=1)
         new_scale = torch.where(den > 0, num / den.clamp_min(1e-30), safe)
         safe = torch.where(new_scale > 0, new_scale, safe)
-        level, path, member, _ = viterbi(w32 / safe[:, None], cb, n_states)
+        level, path, member = search(w32 / safe[:, None])
     scales = torch.where(nonzero, safe, torch.zeros_like(safe))
     return TCQQuantized(level, path, member, scales, cb, bits, n_states)

@@ -31,7 +31,7 @@ from torch import Tensor, nn
 
 from turbopress_amd import hip_kernel as hk
 
-__all__ = ["PackedTCQLinear", "MODES", "Trellis", "trellis_generators"]
+__all__ = ["PackedTCQLinear", "MODES", "Trellis", "trellis_generators", "pack_linear", "pack_model"]
 
 MODES = ("hip", "triton", "cached", "tiled")
 
@@ -248,3 +248,8 @@ class PackedTCQLinear(nn.Module):
                 f"bits={self.bits}, n_states={self.n_states}, mode={self.mode!r}, "
                 f"resident={self.packed_bytes() / 2**20:.1f} MiB "
                 f"(fp16 {2 * self.in_features * self.out_features / 2**20:.1f} MiB)")
+
+
+# The reference's runtime module also holds the compress-time entry points
+# (runtime.py:143-186, 368-411); they live in turbopress_amd.pack.
+from turbopress_amd.pack import pack_linear, pack_model  # noqa: E402
