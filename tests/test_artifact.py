@@ -139,6 +139,25 @@ def test_graph_decode_matches_eager(cuda, tiny_artifact):
 
 
 @pytest.mark.gpu
+def test_graph_decode_from_shared_prefill(cuda, tiny_artifact):
+    """A 16-token prompt (its prefill runs the batched split-K GEMV): eager
+    and graph loops started from copies of one prefill give the same tokens
+    and leave the shared cache and token as they were."""
+    from turbopress_amd.graph_decode import decode_eager, decode_graph, prefill
+    model, _ = load_packed_model(tiny_artifact, device="cuda", mode="hip")
+    ids = torch.randint(0, 1024, (1, 16), generator=torch.Generator().manual_seed(3)).to(cuda)
+    n_new, max_len = 12, 16 + 12 + 8
+    start = prefill(model, ids, max_len)
+    tok0 = start[1].clone()
+    keys0 = [lyr.keys.clone() for lyr in start[0].layers]
+    toks_e, _ = decode_eager(model, ids, n_new, max_len, start=start)
+    toks_g, _ = decode_graph(model, ids, n_new, max_len, start=start)
+    assert toks_e == toks_g and toks_e[0] == int(tok0)
+    assert torch.equal(start[1], tok0)
+    assert all(torch.equal(lyr.keys, k) for lyr, k in zip(start[0].layers, keys0))
+
+
+@pytest.mark.gpu
 def test_fused_shared_input_projections_match(cuda, tiny_artifact):
     """q/k/v and gate/up joined into one launch per group: same logits (to
     the GEMV tolerance) and the same greedy tokens, eager and graph-replayed."""

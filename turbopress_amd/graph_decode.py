@@ -4,18 +4,29 @@ step; the reference's ``scripts/graph_decode_bench.py:39-118``).
 Prefill once, then capture ONE decode step -- static input token, static KV
 cache (``transformers.StaticCache``), device-side cache position -- in a HIP
 graph and replay it per token, so no Python runs between kernels.
-``decode_eager`` is the same loop without capture; the two must produce the
-same greedy tokens.  Every PackedTCQLinear forward is capture-safe (no host
-synchronisation, no allocation outside torch's graph pool).
+``decode_eager`` is the same loop without capture; from the same prefilled
+cache the two produce the same greedy tokens.  Every PackedTCQLinear forward
+is capture-safe (no host synchronisation, no allocation outside torch's
+graph pool).
+
+The prefill runs the prompt as one batch.  Above 8 rows the batched
+decode-GEMV splits K over workgroups and adds their fp32 partial sums with
+atomics in arrival order (as the reference's split-D configurations do,
+``turbopress/triton_kernel.py:126-129``), so two prefills of one prompt can
+differ in the last bits of the cache -- enough to flip a greedy token where
+the top two logits nearly tie.  ``prefill`` therefore runs once and both
+loops start from copies of its cache.  The batch-1 decode steps add in a
+fixed order: their tokens are reproducible.
 """
 
 from __future__ import annotations
 
+import copy
 import time
 
 import torch
 
-__all__ = ["build_static_cache", "decode_eager", "decode_graph"]
+__all__ = ["build_static_cache", "prefill", "decode_eager", "decode_graph"]
 
 
 def build_static_cache(model, max_len: int):
@@ -40,11 +51,28 @@ def _prefill(model, cache, prompt_ids):
 
 
 @torch.inference_mode()
-def decode_eager(model, prompt_ids, n_new: int, max_len: int):
-    """Greedy tokens (n_new of them) and tokens/s of the uncaptured loop."""
+def prefill(model, prompt_ids, max_len: int):
+    """The prompt run into a fresh StaticCache of `max_len` positions:
+    (cache, first greedy token [1, 1])."""
     cache = build_static_cache(model, max_len)
+    return cache, _prefill(model, cache, prompt_ids)
+
+
+def _start(model, prompt_ids, max_len, start):
+    # a private copy of a shared prefill, or a prefill of our own
+    if start is None:
+        return prefill(model, prompt_ids, max_len)
+    cache, tok = start
+    return copy.deepcopy(cache), tok.clone()
+
+
+@torch.inference_mode()
+def decode_eager(model, prompt_ids, n_new: int, max_len: int, start=None):
+    """Greedy tokens (n_new of them) and tokens/s of the uncaptured loop.
+    `start`: a (cache, token) pair from ``prefill`` of this prompt to begin
+    from (copied; the pair is left as it was) instead of prefilling here."""
     n = prompt_ids.shape[1]
-    tok = _prefill(model, cache, prompt_ids)
+    cache, tok = _start(model, prompt_ids, max_len, start)
     out = [int(tok)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -59,13 +87,13 @@ def decode_eager(model, prompt_ids, n_new: int, max_len: int):
 
 
 @torch.inference_mode()
-def decode_graph(model, prompt_ids, n_new: int, max_len: int, warmup: int = 3):
+def decode_graph(model, prompt_ids, n_new: int, max_len: int, warmup: int = 3, start=None):
     """Greedy tokens and tokens/s with one captured decode step replayed per
-    token.  The first `warmup` steps run uncaptured on a side stream."""
-    cache = build_static_cache(model, max_len)
+    token.  The first `warmup` steps run uncaptured on a side stream.
+    `start` as for ``decode_eager``."""
     dev = model.device
     n = prompt_ids.shape[1]
-    static_tok = _prefill(model, cache, prompt_ids).clone()
+    cache, static_tok = _start(model, prompt_ids, max_len, start)
     static_pos = torch.tensor([n], device=dev)
     out = [int(static_tok)]
 
@@ -164,8 +192,10 @@ def main(argv=None) -> int:
     vocab = model.config.vocab_size
     prompt = torch.randint(0, vocab, (1, args.prompt_len), generator=torch.Generator().manual_seed(0)).cuda()
     max_len = args.prompt_len + args.new_tokens + 8
-    toks_e, tps_e = decode_eager(model, prompt, args.new_tokens, max_len)
-    toks_g, tps_g = decode_graph(model, prompt, args.new_tokens, max_len)
+    start = prefill(model, prompt, max_len)
+    toks_e, tps_e = decode_eager(model, prompt, args.new_tokens, max_len, start=start)
+    toks_g, tps_g = decode_graph(model, prompt, args.new_tokens, max_len, start=start)
+    del start
     out = {"model": args.synthetic or str(args.artifact), "mode": args.mode, "fused_groups": args.fuse, "bits": int(meta.get("bits", args.bits)),
            "n_states": int(meta["n_states"]), "prompt_len": args.prompt_len, "new_tokens": args.new_tokens,
            "eager_tok_s": round(tps_e, 1), "graph_tok_s": round(tps_g, 1), "greedy_tokens_match": toks_e == toks_g}
