@@ -170,7 +170,9 @@ __device__ __forceinline__ void store4h(uint16_t* p, const float v[4]) {
 // through `scr` one batch row at a time: H_256 inside every chunk (fp32),
 // then H_(hb/256) across the chunks of each block -- the stages in order of
 // distance, as the reference's transform runs them.
-template <bool ROT, int NPRE>
+// BIG: the kernel variant for blocks above 512 columns (the only one that
+// holds that path's registers); the others take blocks <= 512 only.
+template <bool ROT, bool BIG, int NPRE>
 __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>& f, bool pre, uint16_t* zl, float* scr,
                             int tid, int wave, int lane) {
   const int nch = a.G4;
@@ -183,7 +185,7 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>
     }
     return;
   }
-  if (a.hb <= 2 * kChunkCols) {
+  if constexpr (!BIG) {
     int it0 = wave;
     if (pre) {
 #pragma unroll
@@ -206,83 +208,85 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>
       store4h(zl + b * a.zstride + ci * kChunkCols + lane * 4, v);
     }
     return;
-  }
-  const int m = a.hb / kChunkCols;  // 4, 8 or 16
-  for (int b = 0; b < a.batch; ++b) {
-    const uint16_t* xr = P.x + (size_t)b * P.ldx;
-    for (int ci = wave; ci < nch; ci += kLinWaves) {
-      const int c0 = ci * kChunkCols + lane * 4;
-      const int k = (ci - wave) / kLinWaves;  // prefetched item of row 0
-      float v[4];
-      if (pre && b == 0 && k < NPRE) {
-        // (k < NPRE is uniform: select the registers without indexing)
-        float t[4];
+  } else {
+    const int m = a.hb / kChunkCols;  // 4, 8 or 16
+    for (int b = 0; b < a.batch; ++b) {
+      const uint16_t* xr = P.x + (size_t)b * P.ldx;
+      for (int ci = wave; ci < nch; ci += kLinWaves) {
+        const int c0 = ci * kChunkCols + lane * 4;
+        const int k = (ci - wave) / kLinWaves;  // prefetched item of row 0
+        float v[4];
+        if (pre && b == 0 && k < NPRE) {
+          // (k < NPRE is uniform: select the registers without indexing)
+          float t[4];
 #pragma unroll
-        for (int kk = 0; kk < NPRE; ++kk) {
-          if (kk == k) {
-            lin_pre_product(a, f, kk, ci * kChunkCols, t);
+          for (int kk = 0; kk < NPRE; ++kk) {
+            if (kk == k) {
+              lin_pre_product(a, f, kk, ci * kChunkCols, t);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = t[e];
+              for (int e = 0; e < 4; ++e) v[e] = t[e];
+            }
+          }
+        } else {
+          float xv[4], rv[4];
+          load4h(xr + c0, xv);
+          load4h(P.rs + c0, rv);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = xv[e] * rv[e];
+        }
+        float p = v[0], q = v[1];
+        v[0] = p + q; v[1] = p - q;
+        p = v[2]; q = v[3];
+        v[2] = p + q; v[3] = p - q;
+        p = v[0]; q = v[2];
+        v[0] = p + q; v[2] = p - q;
+        p = v[1]; q = v[3];
+        v[1] = p + q; v[3] = p - q;
+#pragma unroll
+        for (int sft = 0; sft < 6; ++sft) {
+          const bool upper = (lane >> sft) & 1;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float t = __shfl_xor(v[e], 1 << sft, 64);
+            v[e] = upper ? t - v[e] : v[e] + t;
           }
         }
-      } else {
-        float xv[4], rv[4];
-        load4h(xr + c0, xv);
-        load4h(P.rs + c0, rv);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = xv[e] * rv[e];
+        *reinterpret_cast<float4_t*>(scr + c0) = float4_t{v[0], v[1], v[2], v[3]};
       }
-      float p = v[0], q = v[1];
-      v[0] = p + q; v[1] = p - q;
-      p = v[2]; q = v[3];
-      v[2] = p + q; v[3] = p - q;
-      p = v[0]; q = v[2];
-      v[0] = p + q; v[2] = p - q;
-      p = v[1]; q = v[3];
-      v[1] = p + q; v[3] = p - q;
+      __syncthreads();
+      const int items = a.d / m;  // (block, position inside the chunk) pairs
+      for (int it = tid; it < items; it += kLinThreads) {
+        const int h = it / kChunkCols, pos = it - h * kChunkCols;
+        const int base = h * a.hb + pos;
+        float u[16];
 #pragma unroll
-      for (int sft = 0; sft < 6; ++sft) {
-        const bool upper = (lane >> sft) & 1;
+        for (int i = 0; i < 16; ++i) u[i] = i < m ? scr[base + i * kChunkCols] : 0.f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float t = __shfl_xor(v[e], 1 << sft, 64);
-          v[e] = upper ? t - v[e] : v[e] + t;
-        }
-      }
-      *reinterpret_cast<float4_t*>(scr + c0) = float4_t{v[0], v[1], v[2], v[3]};
-    }
-    __syncthreads();
-    const int items = a.d / m;  // (block, position inside the chunk) pairs
-    for (int it = tid; it < items; it += kLinThreads) {
-      const int h = it / kChunkCols, pos = it - h * kChunkCols;
-      const int base = h * a.hb + pos;
-      float u[16];
+        for (int dist = 1; dist < 16; dist <<= 1) {
+          if (dist < m) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) u[i] = i < m ? scr[base + i * kChunkCols] : 0.f;
-#pragma unroll
-      for (int dist = 1; dist < 16; dist <<= 1) {
-        if (dist < m) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            if (!(i & dist)) {
-              const float p = u[i], q = u[i + dist];
-              u[i] = p + q;
-              u[i + dist] = p - q;
+            for (int i = 0; i < 16; ++i) {
+              if (!(i & dist)) {
+                const float p = u[i], q = u[i + dist];
+                u[i] = p + q;
+                u[i + dist] = p - q;
+              }
             }
           }
         }
-      }
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        if (i < m) zl[b * a.zstride + base + i * kChunkCols] = f2h(u[i] / a.hdiv);
+        for (int i = 0; i < 16; ++i)
+          if (i < m) zl[b * a.zstride + base + i * kChunkCols] = f2h(u[i] / a.hdiv);
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 }
 
 // MULTI: 2..4 linears (part of a group is found per tile group); otherwise
 // one linear, whose argument fields sit at fixed offsets and load at once.
-template <int KB, int NS, int SB, bool ROT, bool MULTI>
+// BIG: Hadamard blocks of 1024..4096 columns (lin_stage_z).
+template <int KB, int NS, int SB, bool ROT, bool MULTI, bool BIG>
 __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a) {
   __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
   extern __shared__ __attribute__((aligned(16))) char lin_lds[];
@@ -364,7 +368,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     if (g == (int)blockIdx.x) build_pair_table_lanes<KB>(table, cb_lane, tid, kLinThreads);
     if (p != staged) {
       if (staged >= 0) __syncthreads();  // the previous group's reads of z and scr are done
-      lin_stage_z<ROT, lin_pre(KB)>(a, P, xf, pre, zl, scr, tid, wave, lane);
+      lin_stage_z<ROT, BIG, lin_pre(KB)>(a, P, xf, pre, zl, scr, tid, wave, lane);
       staged = p;
     }
     __syncthreads();
@@ -432,7 +436,13 @@ namespace {
 
 template <int KB, int NS, int SB, bool ROT>
 void launch_linear(const LinArgs& a, int grid, size_t dyn, hipStream_t s) {
-  auto kern = a.n_part > 1 ? tcq_linear_kernel<KB, NS, SB, ROT, true> : tcq_linear_kernel<KB, NS, SB, ROT, false>;
+  // (blocks above 512 columns run their own variant, so that the others
+  // keep that path's registers free: no spill frame, no scratch set-up)
+  const bool big = ROT && a.hb > 2 * kChunkCols;
+  auto kern = big ? (a.n_part > 1 ? tcq_linear_kernel<KB, NS, SB, ROT, true, ROT>
+                                  : tcq_linear_kernel<KB, NS, SB, ROT, false, ROT>)
+                  : (a.n_part > 1 ? tcq_linear_kernel<KB, NS, SB, ROT, true, false>
+                                  : tcq_linear_kernel<KB, NS, SB, ROT, false, false>);
   allow_dynamic_lds(reinterpret_cast<const void*>(kern), kTableBytes + 256);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kLinThreads), dyn, s, a);
 }
