@@ -95,6 +95,21 @@ def tiny_artifact(tmp_path_factory):
 
 
 @pytest.mark.gpu
+def test_load_packed_model_rejects_an_artifact_missing_a_tensor(cuda, tiny_artifact, tmp_path):
+    """The model is built without initialising its parameters, so a tensor
+    the artifact does not hold (here a norm weight) is an error, not
+    silently uninitialised memory."""
+    import shutil
+    bad = tmp_path / "bad"
+    shutil.copytree(tiny_artifact, bad)
+    blob = torch.load(bad / "turbopress_weights.pt", weights_only=True)
+    del blob["extra_state"]["model.norm.weight"]
+    torch.save(blob, bad / "turbopress_weights.pt")
+    with pytest.raises(RuntimeError, match="lacks tensors"):
+        load_packed_model(bad, device="cuda", mode="hip")
+
+
+@pytest.mark.gpu
 def test_load_packed_model_replaces_every_decoder_linear(cuda, tiny_artifact):
     from turbopress_amd.artifact import decoder_layers
     from turbopress_amd.runtime import PackedTCQLinear

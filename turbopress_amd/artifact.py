@@ -105,6 +105,28 @@ def decoder_layers(model: nn.Module):
     raise RuntimeError(f"cannot locate the decoder layers of {type(model).__name__}")
 
 
+def empty_causal_lm(config):
+    """The causal LM of `config` in fp16 on the CPU with its parameters
+    allocated but not filled (transformers' no-init context, as its own
+    checkpoint loading uses): the caller loads or replaces every one.  The
+    random initialisation skipped here takes minutes on the CPU at 4B
+    parameters; buffers computed by the constructors (rotary frequencies,
+    norm weights) are set as usual."""
+    from transformers import AutoModelForCausalLM
+    try:
+        from transformers.initialization import no_init_weights
+    except ImportError:  # older transformers
+        from transformers.modeling_utils import no_init_weights
+    prev_dtype = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with no_init_weights():
+            model = AutoModelForCausalLM.from_config(config)
+    finally:
+        torch.set_default_dtype(prev_dtype)
+    return model.to(dtype=torch.float16)
+
+
 @torch.no_grad()
 def load_packed_model(artifact_dir, *, device: str = "cuda", mode: str = "cached"):
     """Load a TurboPress artifact directory into a packed causal LM
@@ -131,25 +153,26 @@ def load_packed_model(artifact_dir, *, device: str = "cuda", mode: str = "cached
     if not str(device).startswith("cuda") or not torch.cuda.is_available():
         raise RuntimeError("turbopress_amd runs on a ROCm GPU: pass a cuda device")
 
-    from transformers import AutoConfig, AutoModelForCausalLM
+    from transformers import AutoConfig
 
     config = AutoConfig.from_pretrained(root / "hf_config")
-    prev_dtype = torch.get_default_dtype()
-    torch.set_default_dtype(torch.float16)
-    try:
-        model = AutoModelForCausalLM.from_config(config)
-    finally:
-        torch.set_default_dtype(prev_dtype)
-    model = model.to(dtype=torch.float16)
+    model = empty_causal_lm(config)
 
     # Non-quantized tensors; quantized weights and a tied lm_head come back as
     # "missing".  Only a non-".weight" unexpected key is a real mismatch.
-    _missing, unexpected = model.load_state_dict(extra, strict=False)
+    missing, unexpected = model.load_state_dict(extra, strict=False)
     del extra
     unexpected = [k for k in unexpected if not k.endswith(".weight")]
     if unexpected:
         raise RuntimeError(f"unexpected keys in artifact: {unexpected[:8]}")
     model.tie_weights()
+    # The parameters were never initialised: every one must come from the
+    # artifact, be replaced by a packed linear, or be the tied output head.
+    out_emb, in_emb = model.get_output_embeddings(), model.get_input_embeddings()
+    tied = out_emb is not None and in_emb is not None and out_emb.weight is in_emb.weight
+    absent = [k for k in missing if k not in quantized and not (tied and k == "lm_head.weight")]
+    if absent:
+        raise RuntimeError(f"artifact lacks tensors of the model: {absent[:8]}")
 
     for key in list(quantized):
         payload = quantized.pop(key)

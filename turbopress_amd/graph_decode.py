@@ -143,6 +143,10 @@ SYNTHETIC = {
     "qwen3-0.6b": ("qwen3", dict(vocab_size=151936, hidden_size=1024, intermediate_size=3072,
                                  num_hidden_layers=28, num_attention_heads=16, num_key_value_heads=8,
                                  head_dim=128, tie_word_embeddings=True, max_position_embeddings=2048)),
+    # the decoder whose 36 x 7 linears are the headline stack's (config c2)
+    "qwen3-4b": ("qwen3", dict(vocab_size=151936, hidden_size=2560, intermediate_size=9728,
+                               num_hidden_layers=36, num_attention_heads=32, num_key_value_heads=8,
+                               head_dim=128, tie_word_embeddings=True, max_position_embeddings=2048)),
 }
 
 
@@ -160,6 +164,7 @@ def main(argv=None) -> int:
     beside the dense fp16 model of the same shape.  Prints one JSON line."""
     import argparse
     import json
+    import sys
     import tempfile
 
     from turbopress_amd.artifact import load_packed_model
@@ -179,12 +184,17 @@ def main(argv=None) -> int:
                     help="one launch per shared-input group (q/k/v, gate/up) instead of per projection")
     args = ap.parse_args(argv)
 
+    def progress(msg: str) -> None:
+        # (stderr: stdout carries the one JSON line)
+        print(f"[graph_decode] {msg}", file=sys.stderr, flush=True)
+
     with tempfile.TemporaryDirectory() as tmp:
         root = args.artifact
         if args.synthetic:
             root = tmp
             write_synthetic_artifact(root, synthetic_config(args.synthetic), bits=args.bits,
-                                     n_states=args.n_states, seed=0)
+                                     n_states=args.n_states, seed=0, log=progress)
+        progress("loading the packed model")
         model, meta = load_packed_model(root, device="cuda", mode=args.mode)
     if args.fuse:
         from turbopress_amd.decode_step import fuse_shared_input_projections
@@ -203,11 +213,21 @@ def main(argv=None) -> int:
         from transformers import AutoConfig, AutoModelForCausalLM
         del model
         torch.cuda.empty_cache()
+        progress("building the dense fp16 model")
         torch.manual_seed(0)
         config = (synthetic_config(args.synthetic) if args.synthetic
                   else AutoConfig.from_pretrained(f"{args.artifact}/hf_config"))
-        dense = AutoModelForCausalLM.from_config(config)
+        # (random weights initialised on the GPU: a CPU initialisation of a
+        # 4B model takes minutes)
+        prev_dtype = torch.get_default_dtype()
+        torch.set_default_dtype(torch.float16)
+        try:
+            with torch.device("cuda"):
+                dense = AutoModelForCausalLM.from_config(config)
+        finally:
+            torch.set_default_dtype(prev_dtype)
         dense = dense.to(device="cuda", dtype=torch.float16).eval()
+        progress("timing the dense fp16 model")
         out["fp16_eager_tok_s"] = round(decode_eager(dense, prompt, args.new_tokens, max_len)[1], 1)
         out["fp16_graph_tok_s"] = round(decode_graph(dense, prompt, args.new_tokens, max_len)[1], 1)
     print(json.dumps(out), flush=True)

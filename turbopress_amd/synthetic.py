@@ -161,24 +161,23 @@ def tiny_qwen3_config(layers: int = 2, hidden: int = 256, intermediate: int = 76
                        torch_dtype="float16")
 
 
-def write_synthetic_artifact(root, config, bits: int = 3, n_states: int = 64, seed: int = 0) -> dict:
+def write_synthetic_artifact(root, config, bits: int = 3, n_states: int = 64, seed: int = 0,
+                             log=None) -> dict:
     """Write a TurboPress format-v1 artifact directory for a randomly
     initialised model of `config` (pipeline.py:917-931 layout:
     ``turbopress_weights.pt`` = {meta, quantized, extra_state} and
     ``hf_config/``); every decoder linear is a seeded v1 matrix.  Returns the
-    metadata."""
+    metadata.  `log`: optional callable given one progress line per layer."""
     from pathlib import Path
 
     from torch import nn
-    from transformers import AutoModelForCausalLM
 
-    from turbopress_amd.artifact import decoder_layers
+    from turbopress_amd.artifact import decoder_layers, empty_causal_lm
     from turbopress_amd.runtime import trellis_generators
 
     root = Path(root)
     root.mkdir(parents=True, exist_ok=True)
-    torch.manual_seed(seed)
-    model = AutoModelForCausalLM.from_config(config).to(torch.float16)
+    model = empty_causal_lm(config)
     quantized = {}
     prefix = None
     for name, _ in model.named_modules():
@@ -192,7 +191,23 @@ def write_synthetic_artifact(root, config, bits: int = 3, n_states: int = 64, se
                 key = f"{prefix}.{i}.{name}.weight"
                 quantized[key] = make_v1_payload(mod.out_features, mod.in_features, bits, n_states,
                                                  seed=seed * 1000 + len(quantized))
-    extra = {k: v for k, v in model.state_dict().items() if k not in quantized and k != "lm_head.weight"}
+        if log is not None:
+            log(f"synthetic artifact: layer {i + 1}/{len(layers)}")
+    # The other tensors, seeded: embeddings N(0, initializer_range), biases
+    # zero, norm and other 1-D weights one.
+    gen = torch.Generator().manual_seed(seed)
+    std = float(getattr(config, "initializer_range", 0.02))
+    tied = bool(getattr(config, "tie_word_embeddings", False))
+    extra = {}
+    for k, v in model.state_dict().items():
+        if k in quantized or (tied and k == "lm_head.weight"):
+            continue
+        if v.ndim >= 2:
+            extra[k] = (torch.randn(v.shape, generator=gen) * std).to(v.dtype)
+        elif k.endswith(".bias"):
+            extra[k] = torch.zeros(v.shape, dtype=v.dtype)
+        else:
+            extra[k] = torch.ones(v.shape, dtype=v.dtype)
     meta = {"format_version": 1, "model_id": "synthetic", "bits": bits, "n_states": n_states,
             "generators": list(trellis_generators(n_states)), "seed": seed}
     torch.save({"meta": meta, "quantized": quantized, "extra_state": extra}, root / "turbopress_weights.pt")
