@@ -213,17 +213,20 @@ def test_fused_wide_equals_two_launch_path(cuda, batch):
     assert float((fused - two).abs().max()) <= 2e-3 * float(two.abs().max())
 
 
-@pytest.mark.parametrize("shapes,batch", [
-    ([(1024, 2048), (1024, 1024), (1024, 1024)], 1),   # Qwen3-0.6B q/k/v
-    ([(2560, 9728), (2560, 9728)], 1),                 # Qwen3-4B gate/up
-    ([(2560, 4096), (2560, 1024), (2560, 1024)], 5),
+@pytest.mark.parametrize("shapes,batch,bits", [
+    ([(1024, 2048), (1024, 1024), (1024, 1024)], 1, 3),   # Qwen3-0.6B q/k/v
+    ([(2560, 9728), (2560, 9728)], 1, 3),                 # Qwen3-4B gate/up
+    ([(2560, 4096), (2560, 1024), (2560, 1024)], 5, 3),
+    # Hadamard blocks of 1024 / 2048 columns at the other rates
+    ([(1024, 2048), (1024, 1024), (1024, 1024)], 3, 2),
+    ([(2048, 1024), (2048, 512)], 2, 4),
 ])
-def test_group_forward_matches_oracle(cuda, shapes, batch):
+def test_group_forward_matches_oracle(cuda, shapes, batch, bits):
     """tp_packed_linear_forward_group: several linears on one input, one launch."""
     from turbopress_amd import hip_kernel as hk
     from turbopress_amd.runtime import PackedTCQLinear
     d = shapes[0][0]
-    payloads = [make_payload(n, dd, 3, 64, seed=60 + i, bias=(i == 1))
+    payloads = [make_payload(n, dd, bits, 64, seed=60 + i, bias=(i == 1))
                 for i, (dd, n) in enumerate(shapes)]
     lins = [PackedTCQLinear(p, mode="hip") for p in payloads]
     x = make_activation(batch, d, seed=8)
