@@ -475,8 +475,13 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   // Staging issues the activations of lin_pre(bits) items per wave ahead
   // of the weights; each further item costs a dependent round trip, so
   // inputs of more than 3 items per wave (batch * 256-column chunks) keep
-  // the split-K kernel.
-  if (batch * G4 > (int64_t)kLinWaves * (kLinPre + 1) || batch > 4) return kLinearNotHandled;
+  // the split-K kernel -- up to 6 at batch 5..8, where the split-K kernel's
+  // own staging is no cheaper (see the tile condition below).  Blocks above
+  // 512 columns stage one batch row at a time: batch 5..8 keeps the split-K
+  // kernel there.
+  const bool rows8 = batch > 4;
+  if (rows8 && rot && hb > 2 * kChunkCols) return kLinearNotHandled;
+  if (batch * G4 > (int64_t)kLinWaves * (rows8 ? 6 : kLinPre + 1)) return kLinearNotHandled;
 
   // LDS: 64 KiB table (static) + z rows + max(partial sums, one fp32 row).
   const int64_t zstride = G4 * kChunkCols + 8;
@@ -503,6 +508,11 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
     if (groups <= cus || c >= kLinMaxUnits) break;
   }
   if (groups > INT32_MAX / 2) return kLinearNotHandled;
+  // At batch 5..8 every workgroup stages 5..8 input rows: that pays off when
+  // it covers several row tiles (Qwen3-4B gate_proj, k=3: 14.2 -> 11.8 us at
+  // batch 5, 15.6 -> 14.8 us at batch 8), not with one tile per workgroup
+  // (k_proj at batch 8: 10.3 -> 13.3 us).
+  if (rows8 && tpw < 2) return kLinearNotHandled;
 
   LinArgs a;
   a.codebook = codebook;
