@@ -94,14 +94,15 @@ def test_qwen3_4b_forward_matches_tiled_oracle(cuda, name):
 @pytest.mark.parametrize("bits", [2, 3, 4])
 @pytest.mark.parametrize("name", ["gate_proj", "down_proj"])
 def test_c3_mlp_rates_and_batches(cuda, name, bits):
-    """Config 3: Qwen3-4B MLP shapes at k = 2, 3, 4 and batch 1, 4, 8 (one-pass
-    kernel at 1 and 4 where the input fits, split-K kernel otherwise), each
-    batch a separate forward checked against one oracle evaluation."""
+    """Config 3: Qwen3-4B MLP shapes at k = 2, 3, 4 and batch 1, 4, 8 (plus 2
+    and 5: the one-pass kernel where the input fits -- down_proj up to batch
+    2, gate_proj up to 8 --, the split-K kernel otherwise), each batch a
+    separate forward checked against one oracle evaluation."""
     from turbopress_amd.runtime import PackedTCQLinear
     d, n = QWEN3_4B_LAYER[name]
     p = make_payload(n, d, bits, 64, seed=40 + bits)
     lin = PackedTCQLinear(p, mode="hip")
-    xs = [make_activation(b, d, seed=10 * bits + b) for b in (1, 4, 8)]
+    xs = [make_activation(b, d, seed=10 * bits + b) for b in (1, 2, 4, 5, 8)]
     ref = O.tiled_forward(payload_numpy(p), np.concatenate([x.numpy() for x in xs]))
     r0 = 0
     for x in xs:

@@ -473,15 +473,16 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   if (G4 > (int64_t)kLinWaves * kLinMaxUnits) return kLinearNotHandled;
   if (rot && hb > 2 * kChunkCols && G4 * kChunkCols != d) return kLinearNotHandled;
   // Staging issues the activations of lin_pre(bits) items per wave ahead
-  // of the weights; each further item costs a dependent round trip, so
-  // inputs of more than 3 items per wave (batch * 256-column chunks) keep
-  // the split-K kernel -- up to 6 at batch 5..8, where the split-K kernel's
-  // own staging is no cheaper (see the tile condition below).  Blocks above
-  // 512 columns stage one batch row at a time: batch 5..8 keeps the split-K
-  // kernel there.
+  // of the weights; each further item costs a dependent round trip.  Blocks
+  // <= 512 columns take up to 6 items per wave (batch * 256-column chunks)
+  // before the split-K kernel is the faster one (Qwen3-4B down_proj, k=3,
+  // batch 2: 4.75 items, 17.3 -> 14.3 us).  Larger blocks stage one batch
+  // row at a time through LDS: up to 3 items per wave, batch <= 4 (o_proj,
+  // 4096-column blocks, batch 4 at 4 items: 18.0 -> 19.6 us).
   const bool rows8 = batch > 4;
-  if (rows8 && rot && hb > 2 * kChunkCols) return kLinearNotHandled;
-  if (batch * G4 > (int64_t)kLinWaves * (rows8 ? 6 : kLinPre + 1)) return kLinearNotHandled;
+  const bool big = rot && hb > 2 * kChunkCols;
+  if (rows8 && big) return kLinearNotHandled;
+  if (batch * G4 > (int64_t)kLinWaves * (big ? kLinPre + 1 : 6)) return kLinearNotHandled;
 
   // LDS: 64 KiB table (static) + z rows + max(partial sums, one fp32 row).
   const int64_t zstride = G4 * kChunkCols + 8;
