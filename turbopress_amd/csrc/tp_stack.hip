@@ -1344,12 +1344,19 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
   // halo of the range's first unit: word 1 of the previous unit's last segment
   uint32_t x1_last = ch0 > 0 ? pt[((4 * ch0 * kMaxUnitsPerBlock - 1) * kTileRows + r) * 2 + 1] : 0u;
   // the epilogue's row scales and bias (rows 4q..4q+3 of the tile, zeros
-  // past n), loaded now so that they are in registers when the sums are
+  // past n), loaded now so that they are in registers when the sums are --
+  // except in the 4-bit, 32-row, rotating variant, whose registers are full:
+  // there they would be spilled to scratch and reloaded (a round trip of
+  // its own), so they load in the epilogue
+  constexpr bool kEarlyEpilogue = !(KB == 4 && NBT == 2 && ROT);
   const int row0 = t * kTileRows + 4 * q;
   const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(L.scales, (uint32_t)L.n * 2u);
   const __amdgpu_buffer_rsrc_t brs = buffer_rsrc(L.bias, L.bias ? (uint32_t)L.n * 2u : 0u);
-  const u32x2_t sc4 = __builtin_amdgcn_raw_buffer_load_b64(srs, active ? (uint32_t)row0 * 2u : kOutOfRange, 0, 0);
-  const u32x2_t bs4 = __builtin_amdgcn_raw_buffer_load_b64(brs, active ? (uint32_t)row0 * 2u : kOutOfRange, 0, 0);
+  u32x2_t sc4 = {0u, 0u}, bs4 = {0u, 0u};
+  if constexpr (kEarlyEpilogue) {
+    sc4 = __builtin_amdgcn_raw_buffer_load_b64(srs, active ? (uint32_t)row0 * 2u : kOutOfRange, 0, 0);
+    bs4 = __builtin_amdgcn_raw_buffer_load_b64(brs, active ? (uint32_t)row0 * 2u : kOutOfRange, 0, 0);
+  }
   // The first chunk's z, then its weights: the z staging waits for the z
   // loads only, and the weights are in flight during it (and during the
   // table build).
@@ -1403,6 +1410,10 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
   if (!active) return;
 
   // Epilogue: lane holds rows 4q..4q+3 of its tile for batch column r.
+  if constexpr (!kEarlyEpilogue) {
+    sc4 = __builtin_amdgcn_raw_buffer_load_b64(srs, (uint32_t)row0 * 2u, 0, 0);
+    bs4 = __builtin_amdgcn_raw_buffer_load_b64(brs, (uint32_t)row0 * 2u, 0, 0);
+  }
   float v[NBT][4];
 #pragma unroll
   for (int bt = 0; bt < NBT; ++bt)
