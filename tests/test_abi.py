@@ -120,7 +120,7 @@ def test_check_maps_status_to_reference_exceptions():
 
 def test_device_code_indexes_no_register_arrays(tmp_path):
     """Every loop over a register array unrolls to constant indices: the
-    device code holds no VGPR-indexed moves.  (A loop the compiler cannot
+    device code holds no VGPR-indexed moves (and no spills to scratch).  (A loop the compiler cannot
     unroll turns v[e + h] into indexed moves, and once if-converted those
     write past the array into unrelated live registers.)"""
     import shutil
@@ -143,3 +143,10 @@ def test_device_code_indexes_no_register_arrays(tmp_path):
         assert "loop not unrolled" not in log, name
         for insn in ("s_set_gpr_idx_on", "v_movrels", "v_movreld", "v_movrelsd"):
             assert insn not in asm, (name, insn)
+        # No register spills to scratch memory, and no scratch set-up at wave
+        # launch: only the 2-bit per-linear variant for Hadamard blocks above
+        # 512 columns keeps a reserved spill frame (no scratch access).
+        assert "scratch_load" not in asm and "scratch_store" not in asm, name
+        for kern, body in re.findall(r"\.amdhsa_kernel (\S+)\n(.*?)\.end_amdhsa_kernel", asm, re.S):
+            if ".amdhsa_enable_private_segment 1" in body:
+                assert re.search(r"tcq_linear_kernelILi2E.*ELb1ELb0ELb1E", kern), (name, kern)
