@@ -1289,8 +1289,13 @@ __device__ __forceinline__ ZChunk wide_rotate(const XChunk& c, int lane, int hb,
 // One unit of one wave of the wide kernel: decode 64 weights per lane, then
 // for each of the 8 MFMA positions read the B operands of the NBT batch tiles
 // from the staged chunk (rows past the batch hold stale data: their MFMA
-// columns are never written out).
-template <int KB, int NS, int NBT>
+// columns are never written out).  PREB: position p + 1's B reads are issued
+// before position p's MFMAs, so that not every position waits for an LDS
+// round trip (the scheduler would otherwise place each read next to its
+// MFMA to save the registers; batch-32 stack GEMV 524 -> 513 us).  The
+// rotating per-linear variants whose registers are full (4-bit, and 32 rows
+// with 4 trellis states) keep the plain order.
+template <int KB, int NS, int NBT, bool PREB = true>
 __device__ __forceinline__ void wide_unit(const uint2 X, const uint32_t* Mw, const uint32_t x1_last, const int gu,
                                           const int lc, const int q, const int r, const int lane,
                                           const uint32_t laneoff, const uint32_t* table, const uint16_t* zb,
@@ -1300,18 +1305,42 @@ __device__ __forceinline__ void wide_unit(const uint2 X, const uint32_t* Mw, con
   const uint32_t P = ((halo >> 1) & 0x55555555u) | ((X.y << 1) & 0xAAAAAAAAu);
   MemberWords<KB> m[2];
   split_members<KB>(Mw, m);
+  // column offset (halves) of MFMA position pos = 4 x + j in the segment
+  auto boff = [](int pos) { return 16 * (pos >> 2) + (pos & 2 ? 32 : 0) + (pos & 1 ? 8 : 0); };
+  half8_t bcur[NBT];
+  if constexpr (PREB) {
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt)
+      bcur[bt] = *reinterpret_cast<const half8_t*>(zb + zl_index(bt * 16 + r, lc + boff(0)));
+  }
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
     u32x4_t A[4];
     decode_word<KB, NS>(x ? X.y : X.x, x ? X.x : P, m[x], table, laneoff, A);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int off = 16 * x + (j & 2 ? 32 : 0) + (j & 1 ? 8 : 0);
+      const int pos = 4 * x + j;
       const half8_t av = __builtin_bit_cast(half8_t, A[j]);
+      if constexpr (PREB) {
+        half8_t bnext[NBT];
+        if (pos < 7) {
 #pragma unroll
-      for (int bt = 0; bt < NBT; ++bt) {
-        const half8_t b = *reinterpret_cast<const half8_t*>(zb + zl_index(bt * 16 + r, lc + off));
-        acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[bt], 0, 0, 0);
+          for (int bt = 0; bt < NBT; ++bt)
+            bnext[bt] = *reinterpret_cast<const half8_t*>(zb + zl_index(bt * 16 + r, lc + boff(pos + 1)));
+        }
+        __builtin_amdgcn_sched_barrier(0);  // (the reads stay ahead of the MFMAs)
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bcur[bt], acc[bt], 0, 0, 0);
+        if (pos < 7) {
+#pragma unroll
+          for (int bt = 0; bt < NBT; ++bt) bcur[bt] = bnext[bt];
+        }
+      } else {
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) {
+          const half8_t b = *reinterpret_cast<const half8_t*>(zb + zl_index(bt * 16 + r, lc + boff(pos)));
+          acc[bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, b, acc[bt], 0, 0, 0);
+        }
       }
     }
   }
@@ -1388,7 +1417,8 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
       for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
         if (u < ngu) {
           const int gu = gu0 + u;
-          wide_unit<KB, NS, NBT>(regs.X[u], regs.M[u], x1_last, gu, (4 * gu + q - 4 * gu0) * kSegCols, q, r,
+          wide_unit<KB, NS, NBT, !(ROT && (KB == 4 || (NBT == 2 && NS == 4)))>(
+              regs.X[u], regs.M[u], x1_last, gu, (4 * gu + q - 4 * gu0) * kSegCols, q, r,
                                  lane, laneoff, table, zb, acc);
           x1_last = regs.X[u].y;
         }
