@@ -951,12 +951,6 @@ __device__ __forceinline__ void ord_head(OrdRegs<MW, NZ, UMAX>& B, const OrdDesc
   }
 }
 
-// Vector memory operations ord_head issues: 2 + NZ per unit (3 + NZ at 4
-// bits), the halo word and the scales.
-__host__ __device__ constexpr int ord_loads(int bits, int nz, int umax) {
-  return (bits == 4 ? 3 + nz : 2 + nz) * umax + 1 + kOrdFinish;
-}
-
 // The lane's z offsets inside a unit of a block (batch rows past the batch:
 // out of range).
 template <int NZ>
@@ -1105,25 +1099,27 @@ tcq_stack_ordered_kernel(const char* __restrict__ plan_ro, char* __restrict__ pl
     // is open: all workgroups end a phase together, and loads for far-off
     // phases issued then would queue ahead of the stores and loads of the
     // phases that run first.
+    // The last block of the phase in this workgroup counts its tiles as soon
+    // as the y stores of every wave are complete, and only then issues the
+    // next block's loads: issued first, they met a full memory pipeline at
+    // the phase end and held the count back (1297 -> 1245 us per step).
     const bool near = Dn.valid && Dn.ph <= D.ph + 1;
-    if (near) {
+    const bool last = !Dn.valid || Dn.ph != D.ph;
+    if (near && !last) {
       ord_zv<NZ>(zv, Dn, q, slot, bb, batch);
       ord_head<MW, NZ, UMAX>(B, Dn, wave, pv, mv, zv, q, zrs);
     }
     if (tid == 0) done_tiles += (uint32_t)D.nt;
-    if (!Dn.valid || Dn.ph != D.ph) {
-      // Last block of the phase in this workgroup: count its tiles once the
-      // y stores of every wave are complete.  A near block's loads are
-      // already out; the stores are complete once no more than those loads
-      // are outstanding (loads and stores complete in order).
-      if (near)
-        __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(ord_loads(KB, NZ, UMAX)) : "memory");
-      else
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (last) {
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (tid == 0) {
         count_phase_tiles(odone, D.ph, done_tiles);
         done_tiles = 0;
+      }
+      if (near) {
+        ord_zv<NZ>(zv, Dn, q, slot, bb, batch);
+        ord_head<MW, NZ, UMAX>(B, Dn, wave, pv, mv, zv, q, zrs);
       }
     }
     if (Dn.valid && !near) {
