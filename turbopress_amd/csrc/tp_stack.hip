@@ -810,7 +810,9 @@ __device__ inline void wait_phase_replica(const StackRO& P, const uint32_t* odon
       atomicExch(&C->error, 1u);
       break;
     }
-    __builtin_amdgcn_s_sleep(4);
+    // (polls 512 cycles apart: 256 measured 1237 us per ordered step, 512
+    // 1223 us, 1024 1233 us, 64 1276 us)
+    __builtin_amdgcn_s_sleep(8);
   }
 }
 
