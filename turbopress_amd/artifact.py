@@ -168,9 +168,12 @@ def load_packed_model(artifact_dir, *, device: str = "cuda", mode: str = "cached
     model.tie_weights()
     # The parameters were never initialised: every one must come from the
     # artifact, be replaced by a packed linear, or be the tied output head.
+    # (Buffers are set by the constructors as usual.)
     out_emb, in_emb = model.get_output_embeddings(), model.get_input_embeddings()
     tied = out_emb is not None and in_emb is not None and out_emb.weight is in_emb.weight
-    absent = [k for k in missing if k not in quantized and not (tied and k == "lm_head.weight")]
+    params = {name for name, _ in model.named_parameters(remove_duplicate=False)}
+    absent = [k for k in missing
+              if k in params and k not in quantized and not (tied and k == "lm_head.weight")]
     if absent:
         raise RuntimeError(f"artifact lacks tensors of the model: {absent[:8]}")
 
