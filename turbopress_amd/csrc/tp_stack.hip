@@ -1098,15 +1098,16 @@ tcq_stack_ordered_kernel(const char* __restrict__ plan_ro, char* __restrict__ pl
       }
     }
     // The next block's loads go out at once when it belongs to this phase or
-    // the next one.  For a later phase they wait until the phase before it
-    // is open: all workgroups end a phase together, and loads for far-off
-    // phases issued then would queue ahead of the stores and loads of the
-    // phases that run first.
+    // one of the next two (one: 1222 us per step, two: 1217, three: 1221).
+    // For a later phase they wait until the phase before it is open: all
+    // workgroups end a phase together, and loads for far-off phases issued
+    // then would queue ahead of the stores and loads of the phases that run
+    // first.
     // The last block of the phase in this workgroup counts its tiles as soon
     // as the y stores of every wave are complete, and only then issues the
     // next block's loads: issued first, they met a full memory pipeline at
     // the phase end and held the count back (1297 -> 1245 us per step).
-    const bool near = Dn.valid && Dn.ph <= D.ph + 1;
+    const bool near = Dn.valid && Dn.ph <= D.ph + 2;
     const bool last = !Dn.valid || Dn.ph != D.ph;
     if (near && !last) {
       ord_zv<NZ>(zv, Dn, q, slot, bb, batch);
