@@ -191,3 +191,38 @@ def test_fused_shared_input_projections_match(cuda, tiny_artifact):
     toks_e, _ = decode_eager(model, ids, 12, 32)
     toks_g, _ = decode_graph(model, ids, 12, 32)
     assert toks_e == toks_ref and toks_g == toks_ref
+
+
+@pytest.mark.gpu
+def test_qwen3_4b_width_layers_end_to_end(cuda, tmp_path):
+    """Two decoder layers at Qwen3-4B's widths -- the headline stack's
+    linear shapes (hidden 2560, intermediate 9728, 32 x 128 query and
+    8 x 128 key/value heads) -- through the artifact loader: `hip` and
+    `cached` give the same logits, so do the fused q/k/v and gate/up groups,
+    and greedy decode replayed from a captured step equals the eager loop."""
+    from turbopress_amd.decode_step import fuse_shared_input_projections
+    from turbopress_amd.graph_decode import decode_eager, decode_graph, prefill
+    from turbopress_amd.synthetic import tiny_qwen3_config, write_synthetic_artifact
+    cfg = tiny_qwen3_config(layers=2, hidden=2560, intermediate=9728, heads=32, kv_heads=8, head_dim=128,
+                            vocab=4096)
+    write_synthetic_artifact(tmp_path, cfg, bits=3, n_states=64, seed=1)
+    ids = torch.randint(0, 4096, (1, 8), generator=torch.Generator().manual_seed(4)).to(cuda)
+    cached, _ = load_packed_model(tmp_path, device="cuda", mode="cached")
+    with torch.inference_mode():
+        ref = cached(input_ids=ids).logits.float()
+    del cached
+    model, _ = load_packed_model(tmp_path, device="cuda", mode="hip")
+    with torch.inference_mode():
+        got = model(input_ids=ids).logits.float()
+    assert torch.isfinite(got).all()
+    rel = ((got - ref).abs().max() / ref.abs().max()).item()
+    assert rel < 2e-2, rel
+    assert fuse_shared_input_projections(model) == 2 * 2
+    with torch.inference_mode():
+        fused = model(input_ids=ids).logits.float()
+    rel_f = ((fused - got).abs().max() / got.abs().max()).item()
+    assert rel_f < 5e-3, rel_f
+    start = prefill(model, ids, 32)
+    toks_e, _ = decode_eager(model, ids, 12, 32, start=start)
+    toks_g, _ = decode_graph(model, ids, 12, 32, start=start)
+    assert toks_e == toks_g
