@@ -46,6 +46,29 @@ def test_stack_matches_oracle(cuda, ordered, batch):
     assert stack.error() == 0
 
 
+RAGGED = [  # (d, n, phase): odd n, n below one 16-row tile, n one past a tile
+    (2560, 4095, 0), (1024, 1, 0), (576, 17, 1), (2560, 1537, 1), (4096, 33, 2), (1024, 15, 2),
+]
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("ordered", [False, True])
+@pytest.mark.parametrize("batch", [1, 3, 8, 12, 24])
+def test_stack_ragged_rows(cuda, bits, ordered, batch):
+    """Row counts that are odd or not a multiple of 16 (the last row shares
+    its row-scale and bias dword with the row past the end), with bias:
+    every row of every output within 2e-3 of the oracle, in the slot
+    kernel (batch <= 8) and the wide kernel (batch 9..32), phase-ordered or
+    not."""
+    payloads, stack = _build(cuda, RAGGED, batch, bits=bits, ordered=ordered, bias=True)
+    for o in stack.outputs:
+        o.fill_(float("nan"))
+    stack.run()
+    torch.cuda.synchronize()
+    _check(payloads, stack)
+    assert stack.error() == 0
+
+
 def test_stack_k2_and_repeat_runs_reset_counters(cuda):
     payloads, stack = _build(cuda, [(1024, 3072, 0), (3072, 1024, 1), (2048, 1024, 1)], 1, bits=2,
                              ordered=True)

@@ -270,3 +270,31 @@ def test_packed_linear_forward_abi_batch_9_to_32(cuda, d, block, batch, x_offset
     ref = O.tiled_forward(payload_numpy(p), x.numpy())
     assert O.max_rel(y.float().cpu().numpy(), ref) <= GEMV_TOL
     assert int(lin._gemv_ws.count_nonzero()) == 0  # split-K workspace back to zero
+
+
+def _random_case(seed):
+    """A seeded (n, d, bits, n_states, batch): d with Hadamard blocks from 32
+    to 2048 columns, n not a multiple of the 16-row tile, batch 1..32."""
+    rng = np.random.default_rng(1000 + seed)
+    d = int(rng.choice([96, 160, 192, 320, 576, 640, 1024, 1152, 1536, 2048, 2560, 3072]))
+    n = int(rng.integers(1, 70)) * 16 + int(rng.integers(0, 16))
+    bits = int(rng.choice([2, 3, 4]))
+    n_states = int(rng.choice([4, 8, 16, 64]))
+    batch = int(rng.choice([1, 2, 3, 4, 5, 6, 8, 9, 12, 16, 17, 24, 32]))
+    return n, d, bits, n_states, batch
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_shapes_match_oracle(cuda, seed):
+    """PackedTCQLinear.forward at seeded random shapes, rates, trellis sizes
+    and batches (every launch route: one-pass, split-K, wide, rotation
+    launch + GEMV) against the CPU oracle's tiled forward, to the GEMV
+    tolerance."""
+    from turbopress_amd.runtime import PackedTCQLinear
+    n, d, bits, n_states, batch = _random_case(seed)
+    p = make_payload(n, d, bits, n_states, seed=seed, bias=bool(seed % 2))
+    lin = PackedTCQLinear(p, mode="hip")
+    x = make_activation(batch, d, seed=seed)
+    y = lin(x.to(cuda)).float().cpu().numpy()
+    assert y.shape == (batch, n)
+    assert O.max_rel(y, O.tiled_forward(payload_numpy(p), x.numpy())) <= GEMV_TOL, (n, d, bits, n_states, batch)

@@ -362,7 +362,8 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     const uint32_t x1_prev = __builtin_amdgcn_raw_buffer_load_b32(
         prs, (active && u0 > 0) ? pv + 4u : kOutOfRange, (uint32_t)(u0 > 0 ? u0 - 1 : 0) * unit_p, 0);
     const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(P.scales, (uint32_t)P.n * 2u);
-    // rows 4q..4q+3 in one 8-byte load (words past n read as zero)
+    // rows 4q..4q+3 (zero past n; for odd n also row n - 1, which shares its
+    // dword with row n: the epilogue reads that row again)
     const u32x2_t sc = __builtin_amdgcn_raw_buffer_load_b64(srs, (uint32_t)(tt * kTileRows + 4 * q) * 2u, 0, 0);
 
     if (g == (int)blockIdx.x) build_pair_table_lanes<KB>(table, cb_lane, tid, kLinThreads);
@@ -418,7 +419,9 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
         for (int i = 0; i < 4; ++i) {
           const int row = row0 + i;
           if (row >= P.n) continue;
-          uint16_t out = f2h(v[i] * h2f((uint16_t)(sc[i >> 1] >> (16 * (i & 1)))));
+          uint16_t sv = (uint16_t)(sc[i >> 1] >> (16 * (i & 1)));
+          if ((P.n & 1) && row == P.n - 1) sv = gld(P.scales + row);
+          uint16_t out = f2h(v[i] * h2f(sv));
           if (P.bias) out = f2h(h2f(out) + h2f(gld(P.bias + row)));
           gst(P.y + (size_t)bb * P.ldy + row, out);
         }

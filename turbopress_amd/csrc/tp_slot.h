@@ -21,6 +21,22 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uin
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufferFlags);
 }
 
+// fp16 entries row0 .. row0+3 of a per-row vector of n entries (row scales,
+// bias) as two dwords, zero past n and zero when !ok.  A buffer load is
+// range-checked per dword: the one 8-byte load returns zero for a dword that
+// runs past the vector's end, which for odd n holds row n - 1 (with row n);
+// that row is loaded again on its own (2 bytes, inside the range).
+__device__ __forceinline__ u32x2_t load_rows4(__amdgpu_buffer_rsrc_t r, int row0, int n, bool ok) {
+  u32x2_t w = __builtin_amdgcn_raw_buffer_load_b64(r, ok ? (uint32_t)row0 * 2u : kOutOfRange, 0, 0);
+  const int last = n - 1;
+  if (ok && (n & 1) && last >= row0 && last < row0 + 4) {  // (row0 is a multiple of 4: last - row0 is 0 or 2)
+    const uint32_t h = __builtin_amdgcn_raw_buffer_load_b16(r, (uint32_t)last * 2u, 0, 0);
+    if (last - row0 >= 2) w[1] = h;
+    else w[0] = h;
+  }
+  return w;
+}
+
 template <int MW> struct MemberBuf;
 template <> struct MemberBuf<2> {
   typedef u32x2_t type;

@@ -943,8 +943,7 @@ __device__ __forceinline__ void ord_head(OrdRegs<MW, NZ, UMAX>& B, const OrdDesc
 #pragma unroll
   for (int i = 0; i < kOrdFinish; ++i) {
     const int t = wave + i * kWavesPerGroup;
-    B.sc[i] = __builtin_amdgcn_raw_buffer_load_b64(
-        D.srs, t < D.nt ? ((uint32_t)(D.t0 + t) * kTileRows + 4u * (uint32_t)q) * 2u : kOutOfRange, 0, 0);
+    B.sc[i] = load_rows4(D.srs, (D.t0 + t) * kTileRows + 4 * q, D.n, t < D.nt);
   }
   int k = D.k0;
 #pragma unroll
@@ -1383,8 +1382,8 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
   const __amdgpu_buffer_rsrc_t brs = buffer_rsrc(L.bias, L.bias ? (uint32_t)L.n * 2u : 0u);
   u32x2_t sc4 = {0u, 0u}, bs4 = {0u, 0u};
   if constexpr (kEarlyEpilogue) {
-    sc4 = __builtin_amdgcn_raw_buffer_load_b64(srs, active ? (uint32_t)row0 * 2u : kOutOfRange, 0, 0);
-    bs4 = __builtin_amdgcn_raw_buffer_load_b64(brs, active ? (uint32_t)row0 * 2u : kOutOfRange, 0, 0);
+    sc4 = load_rows4(srs, row0, L.n, active);
+    bs4 = load_rows4(brs, row0, L.n, active && L.bias);
   }
   // The first chunk's z, then its weights: the z staging waits for the z
   // loads only, and the weights are in flight during it (and during the
@@ -1441,8 +1440,8 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
 
   // Epilogue: lane holds rows 4q..4q+3 of its tile for batch column r.
   if constexpr (!kEarlyEpilogue) {
-    sc4 = __builtin_amdgcn_raw_buffer_load_b64(srs, (uint32_t)row0 * 2u, 0, 0);
-    bs4 = __builtin_amdgcn_raw_buffer_load_b64(brs, (uint32_t)row0 * 2u, 0, 0);
+    sc4 = load_rows4(srs, row0, L.n, true);
+    bs4 = load_rows4(brs, row0, L.n, L.bias != nullptr);
   }
   float v[NBT][4];
 #pragma unroll
