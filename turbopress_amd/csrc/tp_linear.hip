@@ -295,6 +295,29 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   constexpr int NZ = 8 / SLOTS;
   constexpr uint32_t unit_p = 4u * kTileRows * 8u;       // path bytes per unit of a tile
   constexpr uint32_t unit_m = 4u * kTileRows * MW * 4u;  // member bytes per unit of a tile
+  // Every kernel argument the prologue uses, in one round trip to the
+  // argument segment (one asm statement naming them, before any use; the
+  // memory clobber keeps the loads below it).  Left to the compiler, the
+  // codebook entry's load went first and its address wait held back the
+  // other argument loads, and a multi-linear launch chained one round trip
+  // per part: each ~1-2 us before the first weight load.  The codebook
+  // entry is then the first vector load in flight (see cb_lane).  Not in
+  // the BIG variants: there the forced loads spilled scalar registers and
+  // the launch got slower (c1 q_proj 8.4 -> 8.7 us).
+  const uint16_t* const codebook = a.codebook;
+  if constexpr (BIG) {
+  } else if constexpr (MULTI) {
+    __asm__ volatile("" ::"s"(codebook), "s"(a.d), "s"(a.hb), "s"(a.batch), "s"(a.tpw), "s"(a.zstride),
+                     "s"(a.hdiv), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(a.part[1].g0), "s"(a.part[2].g0),
+                     "s"(a.part[3].g0)
+                     : "memory");
+  } else {
+    const LinPart& P0 = a.part[0];
+    __asm__ volatile("" ::"s"(codebook), "s"(a.d), "s"(a.hb), "s"(a.batch), "s"(a.tpw), "s"(a.zstride),
+                     "s"(a.hdiv), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(P0.path), "s"(P0.member), "s"(P0.x),
+                     "s"(P0.rs), "s"(P0.scales), "s"(P0.n), "s"(P0.T), "s"(P0.g0)
+                     : "memory");
+  }
   uint16_t* zl = reinterpret_cast<uint16_t*>(lin_lds);
   float* scr = reinterpret_cast<float*>(lin_lds + (((size_t)a.batch * a.zstride * 2 + 15) & ~(size_t)15));
 
@@ -307,7 +330,6 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   const uint32_t laneoff = lane_offsets<KB>(lane);
   const uint32_t pv = (uint32_t)(q * kTileRows + r) * 8u;
   const uint32_t mv = (uint32_t)(q * kTileRows + r) * MW * 4u;
-  const uint32_t cb_lane = gld(a.codebook + (lane & ((2 << KB) - 1)));
   // B operand halves of this lane inside a unit's staged z (rows past the
   // batch read row 0: their MFMA columns are never written out).
   const int bbz = bb < a.batch ? bb : 0;
@@ -319,6 +341,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   const uint32_t tile_p = (uint32_t)a.G4 * unit_p;  // path bytes of one tile
   const uint32_t tile_m = (uint32_t)a.G4 * unit_m;  // member bytes of one tile
   int staged = -1;
+  const uint32_t cb_lane = gld(codebook + (lane & ((2 << KB) - 1)));
 
   // One tile group.  The first call (the workgroup's own group; the host
   // gives every workgroup one group when they fit) is a copy of its own, so
@@ -326,16 +349,18 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   // from the merged state of a loop: at the loop head the wait before the
   // weight loads also covered the activation prefetch.
   auto group = [&](const int g) __attribute__((always_inline)) {
+    // The group's linear: the parts' first groups ascend and unused parts
+    // start at `groups`, so it is the number of parts 1.. starting at or
+    // before g.  (Computed from values of one argument round trip, then one
+    // indexed load of that part: a select per part made a dependent round
+    // trip each.)
     int p = 0;
-    LinPart P = a.part[0];
     if constexpr (MULTI) {
 #pragma unroll
-      for (int i = 1; i < kLinMaxParts; ++i)
-        if (i < a.n_part && g >= a.part[i].g0) p = i;
-#pragma unroll
-      for (int i = 1; i < kLinMaxParts; ++i)
-        if (p == i) P = a.part[i];
+      for (int i = 1; i < kLinMaxParts; ++i) p += g >= a.part[i].g0 ? 1 : 0;
+      p = __builtin_amdgcn_readfirstlane(p);
     }
+    const LinPart P = a.part[p];
     const int t = (g - P.g0) * a.tpw + lt;
     const bool active = lt < a.tpw && t < P.T && nu > 0;  // wave-uniform
     const int tt = active ? t : 0;
