@@ -272,7 +272,8 @@ int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears, int bits,
  * overlap on one plan race).  Sizes are read from the plan; `batch` (the
  * plan's batch) and total_blocks (tp_stack_plan_blocks) only size the launch.
  * A launch whose batch tiles cannot hold the plan's batch sets error 2 and
- * does nothing. */
+ * does nothing.  The codebook must be 4-byte aligned (TP_ERR_MISALIGNED
+ * otherwise). */
 int tp_stack_run(void* plan, int64_t batch, const uint16_t* codebook, int bits,
                  int n_states, int ordered, int64_t total_blocks, void* stream);
 

@@ -73,6 +73,9 @@ def test_host_side_argument_validation(built_lib):
     assert built_lib.tp_read_probe(None, 64, fake, None) == _lib.TP_ERR_NULL_POINTER
     assert built_lib.tp_read_probe(fake, 20, fake, None) == _lib.TP_ERR_BAD_DIMS
     assert built_lib.tp_read_probe(ctypes.c_void_p(24), 64, fake, None) == _lib.TP_ERR_MISALIGNED
+    # the stack's codebook is read as dwords through the scalar cache
+    assert built_lib.tp_stack_gemv(ctypes.c_void_p(256), 1, ctypes.c_void_p(258), 3, 64, 0, 1, None) \
+        == _lib.TP_ERR_MISALIGNED
 
 
 def _stack_array(count, n=256, d=256):

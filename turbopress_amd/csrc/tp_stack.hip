@@ -381,6 +381,9 @@ tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
   const int tid = threadIdx.x;
   for (int item = first; item < end; item += step) {
     const TP_CONST RotItem& L = cread(items + item);
+    // the descriptor's fields in one round trip (the size test below, left
+    // alone, had hb loaded first and the rest after its wait)
+    __asm__ volatile("" ::"s"(L.x), "s"(L.rs), "s"(L.k), "s"(L.d), "s"(L.hb) : "memory");
     if ((L.hb > kRotTile) != BIG) continue;  // (uniform)
     float v[kRotEPT];
     if (!BIG) {
@@ -532,10 +535,25 @@ __device__ __forceinline__ void stream_phase_wait(const SlotEnv& E, int li) {
 // 0, published at the end of cur).  The load cursor runs D - 1 units ahead
 // of the decoder, in cur or in nxt.
 template <int KB, int NS, int SB, int D>
-__device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1, uint32_t pend, int* s_tk) {
+__device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1, uint32_t pend, int* s_tk,
+                                            uint32_t* table, const uint16_t* codebook) {
   constexpr int MW = member_words(KB);
   constexpr int SLOTS = 16 / SB;
   constexpr int NZ = 8 / SLOTS;
+  // The first two schedule entries, then every field of their descriptors
+  // that the stream's start reads, one round trip each (see the kernel);
+  // stream_info and the rest read them again from the scalar cache.
+  {
+    const int e0 = cread(E.sched + (blk0 < E.total ? blk0 : 0));
+    const int e1 = cread(E.sched + (blk1 < E.total ? blk1 : 0));
+    __asm__ volatile("" ::"s"(e0), "s"(e1) : "memory");
+    const TP_CONST LinearDesc& L0 = cread(E.P.lin + __builtin_amdgcn_readfirstlane(e0 >> kStackBlockBits));
+    const TP_CONST LinearDesc& L1 = cread(E.P.lin + __builtin_amdgcn_readfirstlane(e1 >> kStackBlockBits));
+    __asm__ volatile("" ::"s"(L0.path), "s"(L0.member), "s"(L0.scales), "s"(L0.z), "s"(L0.n), "s"(L0.T),
+                     "s"(L0.G), "s"(L0.G4), "s"(L1.path), "s"(L1.member), "s"(L1.z), "s"(L1.T), "s"(L1.G),
+                     "s"(L1.G4)
+                     : "memory");
+  }
   BlockInfo cur = stream_info(E, blk0);
   BlockInfo nxt = stream_info(E, blk1);
   if (cur.G4 == 0) return;
@@ -569,6 +587,29 @@ __device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1
 
 #pragma unroll
   for (int k = 0; k < D - 1; ++k) TP_STREAM_ISSUE(k);
+  // The pair table, built while the first units' loads are in flight: built
+  // first, it held every first weight load ~2 us behind the launch's start.
+  // The codebook comes through the scalar cache (2^KB dwords, 4-byte
+  // aligned), so the build waits for no vector load: a lane's entry is
+  // picked from the scalar registers.
+  {
+    constexpr int NW = 1 << KB;  // dwords of 2^(KB+1) fp16 entries
+    const TP_CONST uint32_t* cbw = (const TP_CONST uint32_t*)codebook;
+    uint32_t w[NW];
+#pragma unroll
+    for (int i = 0; i < NW; ++i) {
+      w[i] = cbw[i];
+      // (kept a scalar value: else a select between two of them became a
+      // per-lane vector load, whose wait drained the weight loads)
+      __asm__ volatile("" : "+s"(w[i]));
+    }
+    const int e = E.lane & (2 * NW - 1);
+    uint32_t v = w[0];
+#pragma unroll
+    for (int i = 1; i < NW; ++i) v = (e >> 1) == i ? w[i] : v;
+    build_pair_table_lanes<KB>(table, (e & 1) ? v >> 16 : v & 0xFFFFu, E.tid, kGroupThreads);
+  }
+  __syncthreads();
 
   for (;;) {
 #pragma unroll
@@ -665,6 +706,25 @@ tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
   __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
   __shared__ int s_tk[2];
   constexpr int MW = member_words(KB);
+  // The scalar loads of the launch's start in as few dependent round trips
+  // as their addresses allow: the kernel arguments, then the plan header,
+  // then (in slot_stream) the first two schedule entries, then their
+  // descriptors.  Left to the compiler, most fields waited for the one
+  // before (~8 round trips, ~3 us at a launch's start, when every
+  // workgroup asks for the same lines).  Each asm names the values to load
+  // together; the memory clobber keeps later loads below it.
+  __asm__ volatile("" ::"s"(plan_ro), "s"(plan_rw), "s"(codebook), "s"(ordered), "s"(spin_limit),
+                   "s"(pa.lin_off), "s"(pa.sched_off), "s"(pa.total), "s"(pa.batch)
+                   : "memory");
+  {
+    // (with the header, the codebook's first dword: its line is then in the
+    // scalar cache when the pair table is built, after the first weight
+    // loads -- fetched only then, it queued behind them, ~2 us)
+    const TP_CONST StackInfo& ci = cread(reinterpret_cast<const StackInfo*>(plan_ro));
+    __asm__ volatile("" ::"s"(ci.n_lin), "s"(ci.total_blocks), "s"(ci.n_phases), "s"(ci.batch), "s"(ci.n_rot),
+                     "s"(ci.min_g4), "s"(ci.zbuf_bytes), "s"(cread(reinterpret_cast<const uint32_t*>(codebook)))
+                     : "memory");
+  }
   SlotEnv E;
   E.P = stack_ro(plan_ro);
   E.C = reinterpret_cast<StackCounters*>(plan_rw);
@@ -701,7 +761,6 @@ tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
   E.pv = (uint32_t)(E.q * kTileRows + r) * 8u;        // path byte offset in a unit
   E.mv = (uint32_t)(E.q * kTileRows + r) * MW * 4u;   // member byte offset in a unit
   E.zrs = buffer_rsrc(plan_rw + E.P.zbuf, (uint32_t)cread(E.P.info).zbuf_bytes);
-  const uint32_t cb_lane = gld(codebook + (E.lane & ((2 << KB) - 1)));
 
   // The first three blocks of every workgroup follow from its index: the
   // first weight loads wait for no ticket, and the first ticket atomics
@@ -712,15 +771,13 @@ tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
   const int blk0 = (int)blockIdx.x;
   const int blk1 = (int)(blockIdx.x + gridDim.x);
   uint32_t pend = blockIdx.x + 2u * gridDim.x;  // thread 0: the block after blk1
-  build_pair_table_lanes<KB>(table, cb_lane, E.tid, kGroupThreads);
-  __syncthreads();
   // Register sets: 4 for 4 z columns per lane set (SB = 4), 2 for SB = 8
   // (four z loads per unit); 2 when a block is shorter than the pipeline.
   constexpr int DMAX = SB <= 4 ? kStreamDepth : 2;
   if (cread(E.P.info).min_g4 >= DMAX - 1)
-    slot_stream<KB, NS, SB, DMAX>(E, blk0, blk1, pend, s_tk);
+    slot_stream<KB, NS, SB, DMAX>(E, blk0, blk1, pend, s_tk, table, codebook);
   else
-    slot_stream<KB, NS, SB, 2>(E, blk0, blk1, pend, s_tk);
+    slot_stream<KB, NS, SB, 2>(E, blk0, blk1, pend, s_tk, table, codebook);
 
   // The last workgroup out resets the counters for the next launch.
   if (E.tid == 0) {
@@ -1899,6 +1956,7 @@ extern "C" int tp_stack_rotate(void* plan, int64_t batch, void* stream) {
 extern "C" int tp_stack_gemv(void* plan, int64_t batch, const uint16_t* codebook, int bits,
                              int n_states, int ordered, int64_t total_blocks, void* stream) {
   if (!plan || !codebook) return TP_ERR_NULL_POINTER;
+  if ((uintptr_t)codebook & 3) return TP_ERR_MISALIGNED;  // read as dwords through the scalar cache
   if (total_blocks < 1 || total_blocks > INT32_MAX) return TP_ERR_BAD_DIMS;
   if (batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
   const int spin_limit = 1 << 22;  // ~ seconds of s_sleep polling; ends the wait regardless

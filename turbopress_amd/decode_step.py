@@ -82,7 +82,9 @@ class LinearStack:
                                           nbytes), "stack_plan_init")
         ns = (ctypes.c_int64 * len(lins))(*[lin.out_features for lin in lins])
         self.total_blocks = int(lib.tp_stack_plan_blocks(ns, len(lins)))
-        self.codebook = l0.codebook
+        # (a copy of its own: the GEMV reads the codebook as 4-byte words, and a
+        # fresh allocation is aligned whatever view the linear holds)
+        self.codebook = l0.codebook.detach().clone()
         self.bits, self.n_states = l0.bits, l0.n_states
         self._entries = arr  # keep the host array alive with the plan
 
