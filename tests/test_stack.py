@@ -217,15 +217,15 @@ def test_batch32_stack_mixed_blocks(cuda):
         assert O.max_rel(stack.outputs[i].float().cpu().numpy(), ref) <= GEMV_TOL, shapes[i]
 
 
-def test_stack_rotation_bit_exact(cuda):
+@pytest.mark.parametrize("batch", [3, 9])
+def test_stack_rotation_bit_exact(cuda, batch):
     """The rotation launch's z rows (the plan's last region, one [batch,
     G4 * 256] fp16 block per linear in order) equal the oracle's
     fp16(blockFWHT(x * rot_scale)) bit for bit, zero past d, for Hadamard
-    blocks 4..16384."""
+    blocks 4..16384; batch 9 runs tile items of 4, 4 and 1 rows."""
     from turbopress_amd.decode_step import LinearStack
     from turbopress_amd.runtime import PackedTCQLinear
     ds = [12, 40, 96, 128, 576, 1024, 2048, 2560, 3072, 4096, 6144, 8192, 9728, 16384]
-    batch = 3
     payloads, entries = [], []
     for i, d in enumerate(ds):
         p = make_payload(16, d, 3, 64, seed=400 + i)
