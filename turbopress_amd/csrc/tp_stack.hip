@@ -1245,17 +1245,23 @@ __device__ __forceinline__ ChunkRegs<MW> load_chunk(const LinearDesc& L, const u
   return c;
 }
 
-struct ZChunk {
-  u32x4_t v[2];
+// A staged chunk is 2048 16-byte pieces: NP = 2048 / NT per thread of an
+// NT-thread workgroup.
+template <int NP>
+struct ZChunkN {
+  u32x4_t v[NP];
 };
+typedef ZChunkN<2> ZChunk;
 
-// Thread tid's two 16-byte pieces of chunk ch: piece i = tid + 1024 k is row
-// i / 64, columns 8 (i % 64) ..; rows past the batch are not loaded.
-__device__ __forceinline__ ZChunk wide_load_z(__amdgpu_buffer_rsrc_t zrs, int zld, int batch, int ch, int tid) {
-  ZChunk c;
+// Thread tid's pieces of chunk ch: piece i = tid + NT k is row i / 64,
+// columns 8 (i % 64) ..; rows past the batch are not loaded.
+template <int NT = kWideThreads>
+__device__ __forceinline__ ZChunkN<2048 / NT> wide_load_z(__amdgpu_buffer_rsrc_t zrs, int zld, int batch, int ch,
+                                                          int tid) {
+  ZChunkN<2048 / NT> c;
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int i = tid + kWideThreads * k;
+  for (int k = 0; k < 2048 / NT; ++k) {
+    const int i = tid + NT * k;
     const int row = i >> 6, c8 = (i & 63) * 8;
     const uint32_t off = row < batch ? (uint32_t)(row * zld + ch * kZCols + c8) * 2u : kOutOfRange;
     c.v[k] = __builtin_amdgcn_raw_buffer_load_b128(zrs, off, 0, 0);
@@ -1263,10 +1269,11 @@ __device__ __forceinline__ ZChunk wide_load_z(__amdgpu_buffer_rsrc_t zrs, int zl
   return c;
 }
 
-__device__ __forceinline__ void wide_store_z(uint16_t* zb, const ZChunk& c, int batch, int tid) {
+template <int NT = kWideThreads>
+__device__ __forceinline__ void wide_store_z(uint16_t* zb, const ZChunkN<2048 / NT>& c, int batch, int tid) {
 #pragma unroll
-  for (int k = 0; k < 2; ++k) {
-    const int i = tid + kWideThreads * k;
+  for (int k = 0; k < 2048 / NT; ++k) {
+    const int i = tid + NT * k;
     const int row = i >> 6, c8 = (i & 63) * 8;
     if (row < batch) *reinterpret_cast<u32x4_t*>(zb + zl_index(row, c8)) = c.v[k];
   }
@@ -1402,6 +1409,56 @@ __device__ __forceinline__ void wide_unit(const uint2 X, const uint32_t* Mw, con
   }
 }
 
+// The same unit for two row tiles of one wave (the unit at the same K of
+// both): each B operand read from the staged chunk feeds the MFMAs of both
+// tiles, half the LDS reads of two waves with one tile each.
+template <int KB, int NS, int NBT>
+__device__ __forceinline__ void wide_unit2(const uint2 X0, const uint32_t* M0, const uint32_t x1l0, const uint2 X1,
+                                           const uint32_t* M1, const uint32_t x1l1, const int gu, const int lc,
+                                           const int q, const int r, const int lane, const uint32_t laneoff,
+                                           const uint32_t* table, const uint16_t* zb, float4_t (*acc)[NBT]) {
+  const uint32_t h0 = (uint32_t)__shfl((int)((q == 3) ? (gu == 0 ? 0u : x1l0) : X0.y), (lane + 48) & 63, 64);
+  const uint32_t h1 = (uint32_t)__shfl((int)((q == 3) ? (gu == 0 ? 0u : x1l1) : X1.y), (lane + 48) & 63, 64);
+  const uint32_t P0 = ((h0 >> 1) & 0x55555555u) | ((X0.y << 1) & 0xAAAAAAAAu);
+  const uint32_t P1 = ((h1 >> 1) & 0x55555555u) | ((X1.y << 1) & 0xAAAAAAAAu);
+  MemberWords<KB> m0[2], m1[2];
+  split_members<KB>(M0, m0);
+  split_members<KB>(M1, m1);
+  auto boff = [](int pos) { return 16 * (pos >> 2) + (pos & 2 ? 32 : 0) + (pos & 1 ? 8 : 0); };
+  half8_t bcur[NBT];
+#pragma unroll
+  for (int bt = 0; bt < NBT; ++bt)
+    bcur[bt] = *reinterpret_cast<const half8_t*>(zb + zl_index(bt * 16 + r, lc + boff(0)));
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    u32x4_t A0[4], A1[4];
+    decode_word<KB, NS>(x ? X0.y : X0.x, x ? X0.x : P0, m0[x], table, laneoff, A0);
+    decode_word<KB, NS>(x ? X1.y : X1.x, x ? X1.x : P1, m1[x], table, laneoff, A1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int pos = 4 * x + j;
+      half8_t bnext[NBT];
+      if (pos < 7) {
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt)
+          bnext[bt] = *reinterpret_cast<const half8_t*>(zb + zl_index(bt * 16 + r, lc + boff(pos + 1)));
+      }
+      __builtin_amdgcn_sched_barrier(0);  // (the reads stay ahead of the MFMAs)
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        acc[0][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, A0[j]), bcur[bt],
+                                                            acc[0][bt], 0, 0, 0);
+        acc[1][bt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8_t, A1[j]), bcur[bt],
+                                                            acc[1][bt], 0, 0, 0);
+      }
+      if (pos < 7) {
+#pragma unroll
+        for (int bt = 0; bt < NBT; ++bt) bcur[bt] = bnext[bt];
+      }
+    }
+  }
+}
+
 // Wide block wb of linear L over 512-column chunks [ch0, ch1): z rows at
 // z + b * zld (fp16, zero past d).  The full K range writes y; a part of it
 // adds its sums into the linear's workspace with device-scope atomics, and
@@ -1410,142 +1467,182 @@ __device__ __forceinline__ void wide_unit(const uint2 X, const uint32_t* Mw, con
 // build_table: the pair table is built here (from cb_lane), after the first
 // chunk's z and weight loads are issued, so that neither waits for it.
 // ROT: z is computed from L.x and L.rs chunk by chunk (wide_rotate).
-template <int KB, int NS, int NBT, bool ROT = false>
+template <int KB, int NS, int NBT, bool ROT = false, int TPW = 1>
 __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const uint16_t* z, int zld, int batch,
                            uint16_t* zl, uint32_t* table, uint32_t laneoff, int tid, int wave, int lane,
                            bool build_table = false, uint32_t cb_lane = 0) {
+  // TPW tiles per wave (a workgroup of kWideWaves / TPW waves covers the
+  // block's 16 tiles): tile k of a wave is wb * 16 + wave + k * 16 / TPW.
+  static_assert(TPW == 1 || (TPW == 2 && !ROT), "two tiles per wave: stack (z staged) only");
+  constexpr int NT = kWideThreads / TPW;
+  constexpr int NWV = kWideWaves / TPW;
   constexpr int MW = member_words(KB);
   const int r = lane & 15, q = lane >> 4;
-  const int t = wb * kWideWaves + wave;
-  const bool active = t < L.T;
   const int nch = (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock;
-  const uint32_t* pt = L.path + (size_t)(active ? t : 0) * L.G * (kTileRows * 2);
-  const uint32_t* mt = L.member + (size_t)(active ? t : 0) * L.G * (kTileRows * MW);
+  int t[TPW];
+  bool active[TPW];
+  const uint32_t* pt[TPW];
+  const uint32_t* mt[TPW];
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+    t[k] = wb * kWideWaves + wave + NWV * k;
+    active[k] = t[k] < L.T;
+    pt[k] = L.path + (size_t)(active[k] ? t[k] : 0) * L.G * (kTileRows * 2);
+    mt[k] = L.member + (size_t)(active[k] ? t[k] : 0) * L.G * (kTileRows * MW);
+  }
   const __amdgpu_buffer_rsrc_t zrs = buffer_rsrc(z, (uint32_t)(batch * zld) * 2u);
 
-  float4_t acc[NBT];
+  float4_t acc[TPW][NBT];
 #pragma unroll
-  for (int bt = 0; bt < NBT; ++bt) acc[bt] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int k = 0; k < TPW; ++k)
+#pragma unroll
+    for (int bt = 0; bt < NBT; ++bt) acc[k][bt] = float4_t{0.f, 0.f, 0.f, 0.f};
   // halo of the range's first unit: word 1 of the previous unit's last segment
-  uint32_t x1_last = ch0 > 0 ? pt[((4 * ch0 * kMaxUnitsPerBlock - 1) * kTileRows + r) * 2 + 1] : 0u;
+  uint32_t x1_last[TPW];
+#pragma unroll
+  for (int k = 0; k < TPW; ++k)
+    x1_last[k] = ch0 > 0 ? pt[k][((4 * ch0 * kMaxUnitsPerBlock - 1) * kTileRows + r) * 2 + 1] : 0u;
   // the epilogue's row scales and bias (rows 4q..4q+3 of the tile, zeros
   // past n), loaded now so that they are in registers when the sums are --
   // except in the 4-bit, 32-row, rotating variant, whose registers are full:
   // there they would be spilled to scratch and reloaded (a round trip of
   // its own), so they load in the epilogue
   constexpr bool kEarlyEpilogue = !(KB == 4 && NBT == 2 && ROT);
-  const int row0 = t * kTileRows + 4 * q;
+  int row0[TPW];
+  u32x2_t sc4[TPW], bs4[TPW];
   const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(L.scales, (uint32_t)L.n * 2u);
   const __amdgpu_buffer_rsrc_t brs = buffer_rsrc(L.bias, L.bias ? (uint32_t)L.n * 2u : 0u);
-  u32x2_t sc4 = {0u, 0u}, bs4 = {0u, 0u};
-  if constexpr (kEarlyEpilogue) {
-    sc4 = load_rows4(srs, row0, L.n, active);
-    bs4 = load_rows4(brs, row0, L.n, active && L.bias);
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) {
+    row0[k] = t[k] * kTileRows + 4 * q;
+    sc4[k] = u32x2_t{0u, 0u};
+    bs4[k] = u32x2_t{0u, 0u};
+    if constexpr (kEarlyEpilogue) {
+      sc4[k] = load_rows4(srs, row0[k], L.n, active[k]);
+      bs4[k] = load_rows4(brs, row0[k], L.n, active[k] && L.bias);
+    }
   }
   // The first chunk's z, then its weights: the z staging waits for the z
   // loads only, and the weights are in flight during it (and during the
   // table build).
-  ZChunk c0;
+  ZChunkN<2048 / NT> c0;
   XChunk x0;
   if constexpr (ROT) x0 = wide_load_x(L, batch, ch0, tid);
-  else c0 = wide_load_z(zrs, zld, batch, ch0, tid);
-  ChunkRegs<MW> ra = load_chunk<MW>(L, pt, mt, ch0, q, r);
-  if (build_table) build_pair_table_lanes<KB>(table, cb_lane, tid, kWideThreads);
+  else c0 = wide_load_z<NT>(zrs, zld, batch, ch0, tid);
+  ChunkRegs<MW> ra[TPW];
+#pragma unroll
+  for (int k = 0; k < TPW; ++k) ra[k] = load_chunk<MW>(L, pt[k], mt[k], ch0, q, r);
+  if (build_table) build_pair_table_lanes<KB>(table, cb_lane, tid, NT);
   if constexpr (ROT) c0 = wide_rotate(x0, lane, L.hb, L.hdiv);
-  wide_store_z(zl + (ch0 & 1) * kWideChunkHalves, c0, batch, tid);
+  wide_store_z<NT>(zl + (ch0 & 1) * kWideChunkHalves, c0, batch, tid);
   __syncthreads();
   // Chunk ch: prefetch chunk ch + 1 of z, decode + multiply ch, store the
   // prefetch into the other buffer, one barrier (the next chunk's buffer is
   // full and nobody still reads the one it will overwrite).
-  auto body = [&](int ch, const ChunkRegs<MW>& regs) {
+  auto body = [&](int ch, const ChunkRegs<MW>* regs) {
     const bool more = ch + 1 < ch1;
-    ZChunk nx;
+    ZChunkN<2048 / NT> nx;
     XChunk nxx;
     if (more) {
       if constexpr (ROT) nxx = wide_load_x(L, batch, ch + 1, tid);
-      else nx = wide_load_z(zrs, zld, batch, ch + 1, tid);
+      else nx = wide_load_z<NT>(zrs, zld, batch, ch + 1, tid);
     }
     const uint16_t* zb = zl + (ch & 1) * kWideChunkHalves;
-    if (active) {
+    // (with two tiles, the second is decoded whenever the first is active;
+    // an inactive one reads tile 0's words and is never written out)
+    if (active[0]) {
       const int gu0 = ch * kMaxUnitsPerBlock;
       const int ngu = min(kMaxUnitsPerBlock, L.G4 - gu0);
 #pragma unroll
       for (int u = 0; u < kMaxUnitsPerBlock; ++u) {
         if (u < ngu) {
           const int gu = gu0 + u;
-          wide_unit<KB, NS, NBT, !(ROT && (KB == 4 || (NBT == 2 && NS == 4)))>(
-              regs.X[u], regs.M[u], x1_last, gu, (4 * gu + q - 4 * gu0) * kSegCols, q, r,
-                                 lane, laneoff, table, zb, acc);
-          x1_last = regs.X[u].y;
+          const int lc = (4 * gu + q - 4 * gu0) * kSegCols;
+          if constexpr (TPW == 1) {
+            wide_unit<KB, NS, NBT, !(ROT && (KB == 4 || (NBT == 2 && NS == 4)))>(
+                regs[0].X[u], regs[0].M[u], x1_last[0], gu, lc, q, r, lane, laneoff, table, zb, acc[0]);
+          } else {
+            wide_unit2<KB, NS, NBT>(regs[0].X[u], regs[0].M[u], x1_last[0], regs[1].X[u], regs[1].M[u],
+                                    x1_last[1], gu, lc, q, r, lane, laneoff, table, zb, acc);
+          }
+#pragma unroll
+          for (int k = 0; k < TPW; ++k) x1_last[k] = regs[k].X[u].y;
         }
       }
     }
     if (more) {
       if constexpr (ROT) nx = wide_rotate(nxx, lane, L.hb, L.hdiv);
-      wide_store_z(zl + ((ch + 1) & 1) * kWideChunkHalves, nx, batch, tid);
+      wide_store_z<NT>(zl + ((ch + 1) & 1) * kWideChunkHalves, nx, batch, tid);
     }
     __syncthreads();
   };
   for (int ch = ch0; ch < ch1; ch += 2) {
-    const ChunkRegs<MW> rb = load_chunk<MW>(L, pt, mt, ch + 1 < ch1 ? ch + 1 : ch, q, r);
+    ChunkRegs<MW> rb[TPW];
+#pragma unroll
+    for (int k = 0; k < TPW; ++k) rb[k] = load_chunk<MW>(L, pt[k], mt[k], ch + 1 < ch1 ? ch + 1 : ch, q, r);
     body(ch, ra);
     if (ch + 1 >= ch1) break;
-    ra = load_chunk<MW>(L, pt, mt, ch + 2 < ch1 ? ch + 2 : ch, q, r);
+#pragma unroll
+    for (int k = 0; k < TPW; ++k) ra[k] = load_chunk<MW>(L, pt[k], mt[k], ch + 2 < ch1 ? ch + 2 : ch, q, r);
     body(ch + 1, rb);
   }
-  if (!active) return;
 
-  // Epilogue: lane holds rows 4q..4q+3 of its tile for batch column r.
-  if constexpr (!kEarlyEpilogue) {
-    sc4 = load_rows4(srs, row0, L.n, true);
-    bs4 = load_rows4(brs, row0, L.n, L.bias != nullptr);
-  }
-  float v[NBT][4];
+  // Epilogue: lane holds rows 4q..4q+3 of each of its tiles for batch column r.
 #pragma unroll
-  for (int bt = 0; bt < NBT; ++bt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[bt][i] = acc[bt][i];
-  if (ch0 > 0 || ch1 < nch) {
-    const int ldws = 16 * NBT;
-#pragma unroll
-    for (int bt = 0; bt < NBT; ++bt) {
-      if (bt * 16 + r >= batch) continue;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) atomicAdd(L.ws + (size_t)(row0 + i) * ldws + bt * 16 + r, v[bt][i]);
+  for (int k = 0; k < TPW; ++k) {
+    if (!active[k]) continue;
+    if constexpr (!kEarlyEpilogue) {
+      sc4[k] = load_rows4(srs, row0[k], L.n, true);
+      bs4[k] = load_rows4(brs, row0[k], L.n, L.bias != nullptr);
     }
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    const uint32_t units = (uint32_t)(min(ch1 * kMaxUnitsPerBlock, L.G4) - ch0 * kMaxUnitsPerBlock);
-    uint32_t old = 0;
-    if (lane == 0) old = atomicAdd(L.cnt + t, units);
-    old = (uint32_t)__shfl((int)old, 0, 64);
-    if (old + units != (uint32_t)L.G4) return;
-    // Last contributor: read and clear the sums (also read-modify-write atomics).
+    float v[NBT][4];
 #pragma unroll
     for (int bt = 0; bt < NBT; ++bt)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        v[bt][i] = (bt * 16 + r < batch) ? atomicExch(L.ws + (size_t)(row0 + i) * ldws + bt * 16 + r, 0.f) : 0.f;
-    if (lane == 0) atomicExch(L.cnt + t, 0u);
-  }
+      for (int i = 0; i < 4; ++i) v[bt][i] = acc[k][bt][i];
+    if (ch0 > 0 || ch1 < nch) {
+      const int ldws = 16 * NBT;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = row0 + i;
-    if (row >= L.n) continue;
-    const float sc = h2f((uint16_t)(sc4[i >> 1] >> (16 * (i & 1))));
-    const float bs = h2f((uint16_t)(bs4[i >> 1] >> (16 * (i & 1))));
+      for (int bt = 0; bt < NBT; ++bt) {
+        if (bt * 16 + r >= batch) continue;
 #pragma unroll
-    for (int bt = 0; bt < NBT; ++bt) {
-      const int nb = bt * 16 + r;
-      if (nb >= batch) continue;
-      uint16_t out = f2h(v[bt][i] * sc);
-      if (L.bias) out = f2h(h2f(out) + bs);
-      gst(L.y + (size_t)nb * L.ldy + row, out);
+        for (int i = 0; i < 4; ++i) atomicAdd(L.ws + (size_t)(row0[k] + i) * ldws + bt * 16 + r, v[bt][i]);
+      }
+      __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      const uint32_t units = (uint32_t)(min(ch1 * kMaxUnitsPerBlock, L.G4) - ch0 * kMaxUnitsPerBlock);
+      uint32_t old = 0;
+      if (lane == 0) old = atomicAdd(L.cnt + t[k], units);
+      old = (uint32_t)__shfl((int)old, 0, 64);
+      if (old + units != (uint32_t)L.G4) continue;
+      // Last contributor: read and clear the sums (also read-modify-write atomics).
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          v[bt][i] = (bt * 16 + r < batch) ? atomicExch(L.ws + (size_t)(row0[k] + i) * ldws + bt * 16 + r, 0.f)
+                                           : 0.f;
+      if (lane == 0) atomicExch(L.cnt + t[k], 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = row0[k] + i;
+      if (row >= L.n) continue;
+      const float sc = h2f((uint16_t)(sc4[k][i >> 1] >> (16 * (i & 1))));
+      const float bs = h2f((uint16_t)(bs4[k][i >> 1] >> (16 * (i & 1))));
+#pragma unroll
+      for (int bt = 0; bt < NBT; ++bt) {
+        const int nb = bt * 16 + r;
+        if (nb >= batch) continue;
+        uint16_t out = f2h(v[bt][i] * sc);
+        if (L.bias) out = f2h(h2f(out) + bs);
+        gst(L.y + (size_t)nb * L.ldy + row, out);
+      }
     }
   }
 }
 
-template <int KB, int NS, int NBT>
-__global__ void __launch_bounds__(kWideThreads)
+template <int KB, int NS, int NBT, int TPW = 1>
+__global__ void __launch_bounds__(kWideThreads / TPW)
 tcq_stack_wide_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_rw,
                       const uint16_t* __restrict__ codebook, int ordered, int spin_limit) {
   __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
@@ -1569,7 +1666,7 @@ tcq_stack_wide_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
   const uint32_t cb_lane = gld(codebook + (lane & ((2 << KB) - 1)));
 
   if (tid == 0) s_next = (int)atomicAdd(&C->ticket, 1u);
-  build_pair_table_lanes<KB>(table, cb_lane, tid, kWideThreads);
+  build_pair_table_lanes<KB>(table, cb_lane, tid, kWideThreads / TPW);
   __syncthreads();
   int blk = __builtin_amdgcn_readfirstlane(s_next);
 
@@ -1587,8 +1684,8 @@ tcq_stack_wide_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
         __syncthreads();
       }
     }
-    wide_block<KB, NS, NBT>(L, wb, 0, (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock, L.z, L.G4 * kChunkCols,
-                            batch, zl, table, laneoff, tid, wave, lane);
+    wide_block<KB, NS, NBT, false, TPW>(L, wb, 0, (L.G4 + kMaxUnitsPerBlock - 1) / kMaxUnitsPerBlock, L.z,
+                                        L.G4 * kChunkCols, batch, zl, table, laneoff, tid, wave, lane);
     if (ordered) {
       __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
@@ -1734,9 +1831,11 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
       allow_dynamic_lds(reinterpret_cast<const void*>(kern), kTableBytes + 256);
       hipLaunchKernelGGL(kern, dim3(grid), dim3(kWideThreads), zbytes, s, ro, plan, cb, ordered, spin_limit);
     } else {
-      auto kern = tcq_stack_wide_kernel<KB, NS, 2>;
+      // 17..32 rows: two row tiles per wave, 8 waves (each B operand read
+      // feeds both tiles' MFMAs)
+      auto kern = tcq_stack_wide_kernel<KB, NS, 2, 2>;
       allow_dynamic_lds(reinterpret_cast<const void*>(kern), kTableBytes + 256);
-      hipLaunchKernelGGL(kern, dim3(grid), dim3(kWideThreads), zbytes, s, ro, plan, cb, ordered, spin_limit);
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(kWideThreads / 2), zbytes, s, ro, plan, cb, ordered, spin_limit);
     }
   }
   return launch_status();
