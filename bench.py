@@ -27,7 +27,11 @@ timed region one replay's 252 outputs are compared with the per-linear
 the decoder's phase order enforced on the device (q/k/v | o | gate/up | down
 of each layer, 144 phases, a phase starts after all of the previous one),
 one launch per shared-input group (144 launches) and one launch per linear
-(252 launches, the drop-in PackedTCQLinear.forward path).
+(252 launches, the drop-in PackedTCQLinear.forward path), and
+``chained_step``: a decode step that respects the data dependencies (each
+layer's q/k/v group, o, gate/up group and down each read the output of the
+launch before; down feeds the next layer; decode_step.ChainedDecodeStep),
+checked against the per-linear forward on the inputs each launch read.
 
 ``roofline`` covers the dominant kernel, the stack's GEMV launch
 (tcq_stack_slot_kernel): its algorithmic bytes (the step's bytes minus the
@@ -49,7 +53,8 @@ graph so no call reads cached weights; per case µs, GB/s over the algorithmic
 bytes and over the reference's (k+1)-bit level-stream bytes, the time one
 streaming-read launch of the same byte count takes (``floor_us``) and the
 fraction of HBM peak.  ``c1_layer_stack`` is the Qwen3-0.6B layer's 7 linears
-as one stack (48 distinct layer copies, > 256 MB).
+as one stack (96 distinct layer copies, 575 MB: over twice the 256 MB
+Infinity Cache).
 ``batch32`` is the batch >= 16 path, the MFMA skinny GEMM of configs[4]: the
 same 36-layer stack at batch 32, as time, TFLOP/s and fraction of the
 2.5 PFLOP/s dense fp16 MFMA peak.
@@ -194,6 +199,53 @@ def time_gemv_kernel(stack, steps, warmup, settle_ms=0.0):
     end.record()
     torch.cuda.synchronize()
     return start.elapsed_time(end) / steps * 1e3
+
+
+def chained_step(device, steps: int, warmup: int, settle_ms: float, n_layers: int = N_LAYERS) -> dict:
+    """A data-dependent decode step over 36 Qwen3-4B layers
+    (decode_step.ChainedDecodeStep): in every layer the q/k/v group reads
+    the layer input, o reads q's output, the gate/up group reads o's output,
+    down reads gate's output and feeds the next layer -- 4 launches per
+    layer, each on the previous one's output, one HIP graph per step.  The
+    layers are seeded like the headline's, with each linear's row scales
+    divided by its expected gain (synthetic.unit_gain) so that activations
+    keep their magnitude along the 144 chained projections (a real decoder
+    has RMS norms between them; here fp16 would overflow by layer ~12).  Every
+    output of the captured step is checked against the per-linear forward
+    on the same inputs (the tests check the chain against the oracle)."""
+    from turbopress_amd.decode_step import ChainedDecodeStep
+    from turbopress_amd.runtime import PackedTCQLinear
+    from turbopress_amd.synthetic import QWEN3_4B_LAYER, make_activation, make_payload, unit_gain
+    layers = []
+    for li in range(n_layers):
+        mods = {}
+        for j, name in enumerate(ORDER):
+            d, n = QWEN3_4B_LAYER[name]
+            mods[name] = PackedTCQLinear(unit_gain(make_payload(n, d, BITS, N_STATES, seed=1000 * li + j)),
+                                         mode="hip")
+        layers.append(mods)
+    x = make_activation(BATCH, QWEN3_4B_LAYER["q_proj"][0], seed=7).to(device)
+    chain = ChainedDecodeStep(layers, x)
+    ms, _, _ = time_graph(chain.run, steps, warmup, settle_ms)
+    torch.cuda.synchronize()
+    worst, where = 0.0, None
+    for li in range(n_layers):
+        ins = chain.layer_inputs(li)
+        for name in ORDER:
+            ref = layers[li][name](ins[name]).float()
+            got = chain.outputs[li][name].float()
+            err = float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+            if not err <= worst:  # (a NaN counts as the worst)
+                worst, where = err, f"layer {li} {name}"
+    final = chain.outputs[-1]["down_proj"].float()
+    nbytes = step_bytes(layers)
+    out = {"us_per_step": round(ms * 1e3, 2), "launches_per_step": 4 * n_layers, "bytes_per_step": nbytes,
+           "gbps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+           "parity_vs_per_linear": {"max_rel": worst, "worst": where, "tol": PARITY_TOL, "ok": worst <= PARITY_TOL},
+           "final_rms": round(float(final.pow(2).mean().sqrt()), 4)}
+    del chain, layers
+    torch.cuda.empty_cache()
+    return out
 
 
 def check_stack_outputs(stack, layers, inputs) -> dict:
@@ -446,7 +498,7 @@ def per_linear_sweep(cases=None, min_bytes: float = 320e6, settle_ms: float = 50
     return out
 
 
-def c1_layer_stack(steps: int, warmup: int, settle_ms: float, copies: int = 48) -> dict:
+def c1_layer_stack(steps: int, warmup: int, settle_ms: float, copies: int = 96) -> dict:
     """the Qwen3-0.6B layer's 7 linears (k=3, B=1) as one stack
     launch pair, over `copies` distinct seeded layers (> 256 MB)."""
     from turbopress_amd.synthetic import QWEN3_0_6B_LAYER
@@ -513,6 +565,8 @@ def main() -> int:
                     help="run only the one-linear-at-a-time table (configs c0, c1, c3, c4) and print it")
     ap.add_argument("--cases", default=None,
                     help="with --per-linear: comma-separated cfg:name:in:out:bits:batch cases")
+    ap.add_argument("--only-chained", action="store_true",
+                    help="run only the data-dependent (chained) decode step and print its figures")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: the packed-TCQ decode path is built and measured "
@@ -530,6 +584,10 @@ def main() -> int:
             cases = [(c[0], c[1], int(c[2]), int(c[3]), int(c[4]), int(c[5]))
                      for c in (s.split(":") for s in args.cases.split(","))]
         print(json.dumps({"per_linear": per_linear_sweep(cases, log=log)}), flush=True)
+        return 0
+    if args.only_chained:
+        print(json.dumps({"chained_step": chained_step(dev, max(5, args.steps // 5), 2, args.settle_ms / 2)}),
+              flush=True)
         return 0
     log(f"building {N_LAYERS}x7 packed linears (k={BITS}, S={N_STATES}, batch {BATCH})")
     layers, inputs = build_layers(dev)
@@ -576,8 +634,16 @@ def main() -> int:
 
         ms_p, _, _ = time_graph(per_linear, steps_slow, 2, args.settle_ms / 2)
         log(f"per-linear launches (252/step): {ms_p * 1e3:.1f} us/step")
+        chained = chained_step(dev, steps_slow, 2, args.settle_ms / 2)
+        log(f"chained decode step (144 dependent launches): {chained['us_per_step']} us/step, "
+            f"parity vs per-linear max-rel {chained['parity_vs_per_linear']['max_rel']:.2e}")
+        if not chained["parity_vs_per_linear"]["ok"]:
+            print(json.dumps({"error": "chained step outputs differ from the per-linear forward",
+                              "chained": chained}), flush=True)
+            return 1
         extra = {"phase_ordered_stack_us": round(ms_o * 1e3, 2), "grouped_launches_us": round(ms_g * 1e3, 2),
-                 "per_linear_launches_us": round(ms_p * 1e3, 2)}
+                 "per_linear_launches_us": round(ms_p * 1e3, 2), "chained_step_us": chained["us_per_step"],
+                 "chained_step": chained}
 
     copy_ref = copy_reference(args.copy_mib) if args.copy_mib > 0 and not args.only_primary else None
     if copy_ref:

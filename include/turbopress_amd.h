@@ -155,10 +155,13 @@ int tp_retile(const uint8_t* path, int64_t path_stride, const uint8_t* member,
               int64_t member_stride, int64_t n, int64_t d, int bits,
               uint8_t* path_tiled, uint8_t* member_tiled, void* stream);
 
-/* Bytes of split-K workspace tp_tcq_gemv_tiled needs for n rows at `batch`
- * (0 for invalid sizes: n outside [1, 2^30], batch outside [1, 32]).  The workspace must be zero before the first call;
- * every call leaves it zero again, so one allocation serves any number of
- * calls (and graph replays) on one stream. */
+/* Bytes of workspace tp_tcq_gemv_tiled / tp_packed_linear_forward may use
+ * for n rows at `batch` (0 for invalid sizes: n outside [1, 2^30], batch
+ * outside [1, 32]): the fp32 split-K sums of the batch 5..32 kernels or the
+ * per-part slices of a K-split batch <= 8 launch, and their counters.  The
+ * workspace must be zero before the first call; every call leaves it zero
+ * again, so one allocation serves any number of calls (and graph replays)
+ * on one stream, also of linears of other sizes up to n. */
 int64_t tp_gemv_workspace_bytes(int64_t n, int64_t batch);
 
 /* y[b, r] = fp16(scale[r] * sum_c codebook[level[r, c]] * z[b, c]) (+ bias),
@@ -192,13 +195,15 @@ int tp_packed_linear_forward(const uint16_t* x, int64_t ldx, int64_t batch,
 /* tp_packed_linear_forward without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
- * The split-K workspace (batch 5..32) is a fixed device array inside the
- * library, one per GPU, held until the process ends: n up to 16384 rows at
- * any batch <= 32 (32768 at batch <= 16); larger calls return
- * TP_ERR_WORKSPACE.  Each call clears the part it uses (a small fill kernel)
- * and allocates nothing.  The first call on a device looks the array up
- * (not capturable: make one call per device before capturing).  Calls that
- * overlap on one GPU race. */
+ * The workspace is a fixed device array inside the library (2 MiB + 8 KiB),
+ * one per GPU, held until the process ends: it holds the split-K sums of n
+ * up to 16384 rows at any batch <= 32 (32768 at batch <= 16); a call whose
+ * route would need more returns TP_ERR_WORKSPACE before any launch (calls
+ * whose route needs no workspace, e.g. most batch-1 shapes, have no limit).
+ * Each launch that uses the array is preceded by a fill kernel clearing the
+ * bytes it uses; the call allocates nothing.  The first call on a device
+ * looks the array up (not capturable: make one call per device before
+ * capturing).  Calls that overlap on one GPU race. */
 int tp_packed_linear_forward_noalloc(const uint16_t* x, int64_t ldx, int64_t batch,
                                      const uint16_t* rot_scale, int64_t block,
                                      const uint8_t* path_tiled, const uint8_t* member_tiled,
@@ -240,7 +245,8 @@ typedef struct tp_stack_linear {
   uint16_t* y;                  /* fp16 [batch, ldy] output */
   int64_t ldy;
   int64_t n, d;
-  int32_t phase;                /* dependency phase, non-decreasing along the list */
+  int32_t phase;                /* dependency phase: 0 for the first linear, then equal to or one
+                                   above the previous linear's (no empty phase in between) */
   int32_t reserved;
 } tp_stack_linear;
 

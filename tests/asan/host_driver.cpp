@@ -94,6 +94,12 @@ static void plan_cases() {
     std::vector<tp_stack_linear> B = L;
     B[5].phase = 0;  // decreasing
     EXPECT(tp_stack_plan_bytes(B.data(), (int)B.size(), 3, 1) == 0);
+    B = L;
+    for (size_t i = 7; i < B.size(); ++i) B[i].phase += 1;  // phase 4 left empty
+    EXPECT(tp_stack_plan_bytes(B.data(), (int)B.size(), 3, 1) == 0);
+    B = L;
+    for (auto& l : B) l.phase += 1;  // no phase 0
+    EXPECT(tp_stack_plan_bytes(B.data(), (int)B.size(), 3, 1) == 0);
   }
   {
     std::vector<tp_stack_linear> B = L;
@@ -159,8 +165,17 @@ static void argument_cases() {
                                   nullptr) != TP_OK);
   EXPECT(tp_packed_linear_forward_noalloc(h, 256, 0, h, 256, b, b, h, h, nullptr, 16, 256, 3, 64, o, 16, nullptr) !=
          TP_OK);
-  EXPECT(tp_packed_linear_forward_noalloc(h, 256, 32, h, 256, b, b, h, h, nullptr, 1 << 20, 256, 3, 64, o, 1 << 20,
-                                          nullptr) == TP_ERR_WORKSPACE);
+  EXPECT(tp_packed_linear_forward_noalloc(h, 256, 33, h, 256, b, b, h, h, nullptr, 1 << 20, 256, 3, 64, o, 1 << 20,
+                                          nullptr) == TP_ERR_BAD_DIMS);
+  {
+    // a split-K route (batch 6, 1024-column Hadamard blocks) one word short
+    // of its workspace: refused before any launch
+    const int64_t n = 33000, T = (n + 15) / 16, need = T * 16 * 16 * 4 + T * 4;
+    EXPECT(tp_gemv_workspace_bytes(n, 6) >= need);
+    void* ws = reinterpret_cast<void*>(0xD00000);
+    EXPECT(tp_packed_linear_forward(h, 1024, 6, h, 1024, b, b, h, h, nullptr, n, 1024, 3, 64, o, n, ws, need - 4,
+                                    nullptr) == TP_ERR_WORKSPACE);
+  }
   EXPECT(tp_tcq_viterbi(nullptr, 256, 16, 256, nullptr, 3, 64, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr,
                         0, nullptr) != TP_OK);
   EXPECT(tp_read_probe(nullptr, 64, nullptr, nullptr) != TP_OK);

@@ -101,15 +101,38 @@ def test_stack_plan_size_limits(built_lib):
     assert built_lib.tp_stack_plan_bytes(_stack_array(1), 1, 3, 33) == 0
 
 
-def test_noalloc_rejects_calls_beyond_its_array(built_lib):
-    """The no-allocation forward refuses, on the host, a call whose split-K
-    workspace would exceed its fixed device array (16384 rows at batch 32)."""
+def test_stack_plan_phases_start_at_zero_without_gaps(built_lib):
+    """A phase waits for the one before it only, so plans whose phases skip
+    a number (or do not start at 0) are refused on the host."""
+    arr = _stack_array(4)
+    for i, ph in enumerate((0, 0, 1, 2)):
+        arr[i].phase = ph
+    assert built_lib.tp_stack_plan_bytes(arr, 4, 3, 1) > 0
+    arr[3].phase = 3  # phase 2 empty
+    assert built_lib.tp_stack_plan_bytes(arr, 4, 3, 1) == 0
+    for i, ph in enumerate((1, 1, 2, 3)):
+        arr[i].phase = ph
+    assert built_lib.tp_stack_plan_bytes(arr, 4, 3, 1) == 0
+
+
+def test_split_k_route_reports_a_short_workspace_before_any_launch(built_lib):
+    """A call routed to the split-K kernel (batch 6 with 1024-column Hadamard
+    blocks: not the one-pass kernel) whose workspace is one word short
+    returns TP_ERR_WORKSPACE on the host, before any launch; the no-allocation
+    forward uses the same routing with its fixed array, whose limit the GPU
+    test checks.  Out-of-range batches are refused first."""
     from turbopress_amd import _lib
     fake = ctypes.c_void_p(256)
-    args = [fake, 256, 32, fake, 256, fake, fake, fake, fake, None, 16400, 256, 3, 64, fake, 16400, None]
-    assert built_lib.tp_packed_linear_forward_noalloc(*args) == _lib.TP_ERR_WORKSPACE
-    args[2] = 33
-    assert built_lib.tp_packed_linear_forward_noalloc(*args) == _lib.TP_ERR_BAD_DIMS
+    n, d, batch = 33000, 1024, 6
+    T = (n + 15) // 16
+    need = T * 16 * 16 * 4 + T * 4  # split-K sums (batch <= 16) + counters
+    assert built_lib.tp_gemv_workspace_bytes(n, batch) >= need
+    args = [fake, d, batch, fake, 1024, fake, fake, fake, fake, None, n, d, 3, 64, fake, n, fake, need - 4, None]
+    assert built_lib.tp_packed_linear_forward(*args) == _lib.TP_ERR_WORKSPACE
+    args[16] = None
+    assert built_lib.tp_packed_linear_forward(*args) == _lib.TP_ERR_WORKSPACE
+    noalloc = [fake, 256, 33, fake, 256, fake, fake, fake, fake, None, 16400, 256, 3, 64, fake, 16400, None]
+    assert built_lib.tp_packed_linear_forward_noalloc(*noalloc) == _lib.TP_ERR_BAD_DIMS
 
 
 def test_check_maps_status_to_reference_exceptions():

@@ -122,6 +122,37 @@ def test_load_packed_model_replaces_every_decoder_linear(cuda, tiny_artifact):
 
 
 @pytest.mark.gpu
+def test_load_packed_model_triton_mode_passes_reference_script_checks(cuda, tiny_artifact):
+    """A model loaded with mode="triton" (what the reference's loader script
+    passes, scripts/bench_packed.py:261) passes that script's three checks on
+    every decoder module (bench_packed.py:286-293): mode is still "triton",
+    the packed stream is held, no fp16 weight cache exists -- and it computes
+    the same logits as mode="hip"."""
+    from turbopress_amd.artifact import decoder_layers
+    from turbopress_amd.runtime import PackedTCQLinear
+    model, _ = load_packed_model(tiny_artifact, device="cuda", mode="triton")
+    count, residual = 0, []
+    for i, block in enumerate(decoder_layers(model)):
+        for name, module in block.named_modules():
+            if isinstance(module, PackedTCQLinear):
+                count += 1
+                assert module.mode == "triton", f"model.layers.{i}.{name} is not in Triton mode."
+                assert module.levels_packed is not None, f"model.layers.{i}.{name} has no packed level stream."
+                assert module._w_cache is None, f"model.layers.{i}.{name} contains an FP16 weight cache."
+            elif isinstance(module, torch.nn.Linear):
+                residual.append(name)
+    assert count == 7 * len(decoder_layers(model)) and not residual
+    ids = torch.randint(0, 1024, (1, 8), generator=torch.Generator().manual_seed(3)).to(cuda)
+    with torch.inference_mode():
+        a = model(input_ids=ids).logits.float()
+    del model
+    hip_model, _ = load_packed_model(tiny_artifact, device="cuda", mode="hip")
+    with torch.inference_mode():
+        b = hip_model(input_ids=ids).logits.float()
+    assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
 def test_packed_model_logits_hip_vs_cached(cuda, tiny_artifact):
     """The bandwidth path (fused rotation + decode-GEMV) and load-time
     decompression (decode + fold + GEMM) give the same model."""

@@ -58,8 +58,8 @@ def test_stack_ragged_rows(cuda, bits, ordered, batch):
     """Row counts that are odd or not a multiple of 16 (the last row shares
     its row-scale and bias dword with the row past the end), with bias:
     every row of every output within 2e-3 of the oracle, in the slot
-    kernel (batch <= 8) and the wide kernel (batch 9..32), phase-ordered or
-    not."""
+    kernel (batch <= 4), the wide kernel (batch 5..32) and, phase-ordered at
+    batch <= 4, the ordered kernel."""
     payloads, stack = _build(cuda, RAGGED, batch, bits=bits, ordered=ordered, bias=True)
     for o in stack.outputs:
         o.fill_(float("nan"))
@@ -147,6 +147,10 @@ def test_stack_rejects_mixed_codebooks(cuda):
         LinearStack([(a, x, 0), (b, x, 0)])
     with pytest.raises(ValueError):
         LinearStack([(a, x, 1), (a, x, 0)])  # phases must not decrease
+    with pytest.raises(ValueError):
+        LinearStack([(a, x, 0), (a, x, 2)])  # nor skip a phase
+    with pytest.raises(ValueError):
+        LinearStack([(a, x, 1), (a, x, 1)])  # and start at 0
 
 
 def test_headline_plan_matches_per_linear_and_oracle(cuda):
@@ -247,3 +251,51 @@ def test_stack_rotation_bit_exact(cuda, batch):
         ref = O.rotate_activations(payload_numpy(p), x.cpu().numpy()).astype(np.float16).view(np.uint16)
         assert np.array_equal(got[:, :d], ref), (d, int(p["block"]))
         assert not got[:, d:].any(), d
+
+
+@pytest.mark.parametrize("shapes", ["qwen3-0.6b", "qwen3-4b"])
+def test_chained_step_matches_oracle_layer_by_layer(cuda, shapes):
+    """The data-dependent decode step (q/k/v group -> o -> gate/up group ->
+    down -> next layer, 4 launches per layer) captured in a graph and
+    replayed on a new input: every projection of every layer within the
+    GEMV tolerance of the oracle on the input that launch read (the previous
+    launch's GPU output), so the chain passes data, and o / gate / down
+    really consume q / o / gate."""
+    from turbopress_amd.decode_step import ChainedDecodeStep
+    from turbopress_amd.runtime import PackedTCQLinear
+    from turbopress_amd.synthetic import QWEN3_0_6B_LAYER, unit_gain
+    table = QWEN3_0_6B_LAYER if shapes == "qwen3-0.6b" else QWEN3_4B_LAYER
+    n_layers = 3 if shapes == "qwen3-0.6b" else 2
+    names = ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")
+    payloads, layers = [], []
+    for li in range(n_layers):
+        ps, mods = {}, {}
+        for j, name in enumerate(names):
+            d, n = table[name]
+            p = unit_gain(make_payload(n, d, 3, 64, seed=500 * li + j, bias=(name == "o_proj")))
+            ps[name], mods[name] = p, PackedTCQLinear(p, mode="hip")
+        payloads.append(ps)
+        layers.append(mods)
+    x = make_activation(1, table["q_proj"][0], seed=3).to(cuda)
+    chain = ChainedDecodeStep(layers, x)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        chain.run()
+    torch.cuda.current_stream().wait_stream(s)
+    with torch.cuda.graph(g):
+        chain.run()
+    x.copy_(make_activation(1, table["q_proj"][0], seed=4).to(cuda))
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    for li in range(n_layers):
+        ins = chain.layer_inputs(li)
+        for name in names:
+            got = chain.outputs[li][name].float().cpu().numpy()
+            ref = O.tiled_forward(payload_numpy(payloads[li][name]), ins[name].float().cpu().numpy())
+            assert O.max_rel(got, ref) <= GEMV_TOL, (li, name)
+    assert torch.equal(chain.layer_inputs(1)["q_proj"], chain.outputs[0]["down_proj"])
+    with pytest.raises(ValueError):
+        ChainedDecodeStep([layers[0], {**layers[1], "q_proj": layers[1]["o_proj"]}], x)

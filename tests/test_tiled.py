@@ -14,6 +14,7 @@ import pytest
 import torch
 
 from oracle import tcq_oracle as O
+from turbopress_amd import hip_kernel as hk
 from turbopress_amd.synthetic import (
     QWEN3_4B_LAYER, make_activation, make_payload, payload_numpy)
 
@@ -125,7 +126,7 @@ def test_c4_batch32(cuda, name):
     for _ in range(2):
         y = lin(x.to(cuda)).float().cpu().numpy()
         assert O.max_rel(y, ref) <= GEMV_TOL
-    assert int(lin._gemv_ws.count_nonzero()) == 0
+    assert int(hk.shared_workspace(cuda, 0).count_nonzero()) == 0
 
 
 def test_workspace_returns_to_zero_and_calls_repeat(cuda):
@@ -135,7 +136,7 @@ def test_workspace_returns_to_zero_and_calls_repeat(cuda):
     x = make_activation(2, 9728, seed=4).to(cuda)
     ys = [lin(x) for _ in range(3)]
     torch.cuda.synchronize()
-    assert int(lin._gemv_ws.count_nonzero()) == 0
+    assert int(hk.shared_workspace(cuda, 0).count_nonzero()) == 0
     for y in ys[1:]:
         assert float((y.float() - ys[0].float()).abs().max()) <= 2e-3 * float(ys[0].float().abs().max())
     ref = O.tiled_forward(payload_numpy(p), x.cpu().numpy())
@@ -238,6 +239,65 @@ def test_group_forward_matches_oracle(cuda, shapes, batch, bits):
         assert O.max_rel(o.float().cpu().numpy(), ref) <= GEMV_TOL
 
 
+def test_shared_workspace_two_linears_back_to_back(cuda):
+    """Two linears of different shapes take turns on the one split-K
+    workspace of the stream (batch 12 and 24: both split K), then a grouped
+    launch gives each member a disjoint region of it; every output matches
+    the oracle and the workspace is zero after each launch.  No linear holds
+    a workspace of its own."""
+    from turbopress_amd.runtime import PackedTCQLinear
+    shapes = [(9728, 2560, 12), (2560, 9728, 24), (9728, 2560, 24)]
+    lins, ps = [], []
+    for i, (n, d, _) in enumerate(shapes):
+        ps.append(make_payload(n, d, 3, 64, seed=300 + i, bias=(i == 1)))
+        lins.append(PackedTCQLinear(ps[-1], mode="hip"))
+        assert not any(t.numel() > 0 and name.endswith("ws") for name, t in lins[-1].named_buffers())
+    for rnd in range(2):
+        for lin, p, (n, d, batch) in zip(lins, ps, shapes):
+            x = make_activation(batch, d, seed=10 * rnd + batch)
+            y = lin(x.to(cuda))
+            torch.cuda.synchronize()
+            assert int(hk.shared_workspace(cuda, 0).count_nonzero()) == 0, (rnd, n, d)
+            ref = O.tiled_forward(payload_numpy(p), x.numpy())
+            assert O.max_rel(y.float().cpu().numpy(), ref) <= GEMV_TOL, (rnd, n, d, batch)
+    # a group of two linears sharing the input (disjoint workspace regions)
+    x = make_activation(12, 2560, seed=99)
+    outs = hk.forward_group([lins[0], lins[2]], x.to(cuda))
+    torch.cuda.synchronize()
+    assert int(hk.shared_workspace(cuda, 0).count_nonzero()) == 0
+    for y, p in zip(outs, (ps[0], ps[2])):
+        assert O.max_rel(y.float().cpu().numpy(), O.tiled_forward(payload_numpy(p), x.numpy())) <= GEMV_TOL
+
+
+KSPLIT_CASES = [  # (n, d, batch): K long against the rows (down_proj and kin), Hadamard blocks <= 512
+    (2560, 9728, 1), (2560, 9728, 2), (2560, 9728, 4), (2560, 9728, 8),
+    (1024, 3584, 4), (333, 4864, 3), (1537, 2624, 8), (96, 9728, 5)]
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("n,d,batch", KSPLIT_CASES)
+def test_ksplit_shapes_match_oracle_deterministically(cuda, bits, n, d, batch):
+    """Shapes whose K range is long against their rows, where the one-pass
+    forward cuts K into parts of whole Hadamard blocks summed through the
+    shared workspace (n odd or not a multiple of 16, d not a multiple of
+    256, bias): outputs within the GEMV tolerance of the oracle, a second
+    call bit-identical to the first (the parts are added in a fixed order),
+    and the workspace zero after each call."""
+    from turbopress_amd.runtime import PackedTCQLinear
+    p = make_payload(n, d, bits, 64, seed=n + d + batch, bias=bool(n % 2))
+    lin = PackedTCQLinear(p, mode="hip")
+    x = make_activation(batch, d, seed=batch).to(cuda)
+    y1 = lin(x)
+    torch.cuda.synchronize()
+    assert int(hk.shared_workspace(cuda, 0).count_nonzero()) == 0
+    y2 = lin(x)
+    torch.cuda.synchronize()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    assert int(hk.shared_workspace(cuda, 0).count_nonzero()) == 0
+    ref = O.tiled_forward(payload_numpy(p), x.cpu().numpy())
+    assert O.max_rel(y1.float().cpu().numpy(), ref) <= GEMV_TOL, (n, d, bits, batch)
+
+
 @pytest.mark.parametrize("d,block", [(3072, 1024), (4096, 4096), (2560, 512)])
 @pytest.mark.parametrize("batch", [12, 20])
 @pytest.mark.parametrize("x_offset", [0, 8])
@@ -261,15 +321,16 @@ def test_packed_linear_forward_abi_batch_9_to_32(cuda, d, block, batch, x_offset
     assert xs.data_ptr() % 16 == x_offset
     y = torch.full((batch, n), float("nan"), dtype=torch.float16, device=cuda)
     buf, pb = lin.tiled_packed, lin._tiled_geo["path_bytes"]
+    ws = hk.gemv_workspace(n, 32, cuda)
     st = _lib.lib().tp_packed_linear_forward(
         xs.data_ptr(), d, batch, lin.rot_scale.data_ptr(), block, buf.data_ptr(), buf.data_ptr() + pb,
         lin.scales.data_ptr(), lin.codebook.data_ptr(), lin.bias.data_ptr(), n, d, 3, 64, y.data_ptr(), n,
-        lin._gemv_ws.data_ptr(), lin._gemv_ws.numel(), torch.cuda.current_stream(cuda).cuda_stream)
+        ws.data_ptr(), ws.numel(), torch.cuda.current_stream(cuda).cuda_stream)
     assert st == 0
     torch.cuda.synchronize()
     ref = O.tiled_forward(payload_numpy(p), x.numpy())
     assert O.max_rel(y.float().cpu().numpy(), ref) <= GEMV_TOL
-    assert int(lin._gemv_ws.count_nonzero()) == 0  # split-K workspace back to zero
+    assert int(ws.count_nonzero()) == 0  # split-K workspace back to zero
 
 
 def _random_case(seed):

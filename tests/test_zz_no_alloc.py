@@ -6,6 +6,7 @@ import pytest
 import torch
 
 from oracle import tcq_oracle as O
+from turbopress_amd import hip_kernel as hk
 from turbopress_amd.synthetic import make_activation, make_payload, payload_numpy
 
 pytestmark = pytest.mark.gpu
@@ -34,12 +35,18 @@ def test_noalloc_matches_workspace_entry_point(cuda):
     from turbopress_amd import _lib
     from turbopress_amd.runtime import PackedTCQLinear
     lib = _lib.lib()
-    cases = [(9728, 2560, 12, 3), (1024, 2560, 6, 4), (2560, 9728, 1, 3)]  # (n, d, batch, bits)
+    # (n, d, batch, bits): split-K at batch 12, then a smaller batch-6 call;
+    # batch 1 (one-pass, no workspace); down_proj at batch 4 (K cut into
+    # parts summed through the array); 1024-column Hadamard blocks at batch
+    # 4 (the split-K kernel at batch <= 4); 32768 rows at batch 16 (the
+    # array's documented limit: the wide kernel's sums fill it exactly)
+    cases = [(9728, 2560, 12, 3), (1024, 2560, 6, 4), (2560, 9728, 1, 3), (2560, 9728, 4, 3),
+             (512, 4096, 4, 3), (32768, 2560, 16, 3), (2560, 9728, 2, 2)]
     for i, (n, d, batch, bits) in enumerate(cases):
         p = make_payload(n, d, bits, 64, seed=70 + i, bias=(i == 1))
         lin = PackedTCQLinear(p, mode="hip")
         x = make_activation(batch, d, seed=80 + i).to(cuda)
-        y_ref = _call(lib, "tp_packed_linear_forward", lin, x, lin._gemv_ws)
+        y_ref = _call(lib, "tp_packed_linear_forward", lin, x, hk.gemv_workspace(n, 32, cuda))
         y = _call(lib, "tp_packed_linear_forward_noalloc", lin, x)
         torch.cuda.synchronize()
         ref = y_ref.float()

@@ -15,6 +15,16 @@
 //     operands from LDS, and no second launch or global z buffer is needed;
 //   * the chunks of a tile are summed through LDS (no atomics, no workspace)
 //     and chunk 0's wave writes y = fp16(sum * scale) (+ bias).
+//   * K-split (one linear, Hadamard blocks <= 512 columns): for shapes whose
+//     K range is long against their rows (down_proj: 160 row tiles x 38
+//     units), the K range is also cut into `kparts` parts of whole Hadamard
+//     blocks, one workgroup per (tile group, part), so that each workgroup
+//     stages and rotates only its part of the input and every CU gets work.
+//     A part's sum is stored with coherent (L2-bypassing) stores into its
+//     own slice of the caller's workspace; the last part to arrive at the
+//     tile's counter adds the slices in part order (a fixed order: the
+//     result does not depend on which workgroup finishes last), writes y,
+//     and leaves slices and counter zero.
 // The per-unit decode and MFMA step is the stack kernel's (tp_slot.h).
 #include "tp_slot.h"
 
@@ -25,6 +35,14 @@ constexpr int kLinThreads = 64 * kLinWaves;
 constexpr int kLinMaxUnits = 3;                      // units per wave, all loaded up front
 constexpr int kLinMaxParts = kMaxInlineLinears;
 constexpr int kLinRedBytes = kLinWaves * 64 * 16;    // one float4 per lane and wave
+// K-split: a part's sums of one row tile are [16 rows][8 batch columns] fp32
+// (512 bytes); at most kLinMaxTileParts (row tile, part) slices per call.
+constexpr int kLinSliceFloats = kTileRows * 8;
+constexpr int kLinMaxTileParts = 2048;
+constexpr int kLinMaxKParts = 16;    // (one register per part in the reduction)
+// Cache policy of buffer accesses that must be coherent across the chip's
+// L2s (sc1, as agent-scope atomic loads and stores compile to).
+constexpr int kCoherent = 16;
 
 struct LinPart {
   const uint32_t* path;      // tiled path words [T][G][16][2]
@@ -45,8 +63,11 @@ struct LinArgs {
   int32_t n_part, groups;    // tile groups over all linears
   int32_t d, G4, hb, batch;  // batch: rows of this launch (<= SB)
   int32_t c, s, tpw;         // units per chunk, chunks per tile, tiles per group
-  int32_t zstride;           // halves per staged z row (G4 * 256 + 8: rows start 4 banks apart)
+  int32_t zstride;           // halves per staged z row (units staged * 256 + 8: rows start 4 banks apart)
   float hdiv;                // sqrt(hb)
+  int32_t kparts, pu;        // K parts per tile group (1: no split), units per part
+  float* kws;                // K-split slices [kparts][T][16 rows][8] fp32 (zero between calls)
+  uint32_t* kcnt;            // K-split arrival counter per row tile (zero between calls)
 };
 
 // Butterflies of one chunk (four columns per lane, lane-major) up to
@@ -118,19 +139,21 @@ struct XPre {
   u32x2_t x[NPRE][2], r[NPRE][2];
 };
 
+// Items of the K part [pu0, pu0 + npu) (units = 256-column chunks).
 template <int NPRE>
-__device__ __forceinline__ XPre<NPRE> lin_prefetch_x(const LinArgs& a, const LinPart& P, int wave, int lane) {
+__device__ __forceinline__ XPre<NPRE> lin_prefetch_x(const LinArgs& a, const LinPart& P, int pu0, int npu, int wave,
+                                                     int lane) {
   XPre<NPRE> f;
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(P.x, (uint32_t)((a.batch - 1) * P.ldx + a.d) * 2u);
   const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(P.rs, (uint32_t)a.d * 2u);
   const bool small = a.hb <= 2 * kChunkCols;
-  const int items = (small ? a.batch : 1) * a.G4;
+  const int items = (small ? a.batch : 1) * npu;
 #pragma unroll
   for (int k = 0; k < NPRE; ++k) {
     const int it = wave + kLinWaves * k;
     const bool ok = it < items;
-    const int b = ok ? it / a.G4 : 0;
-    const int cs = (ok ? it - b * a.G4 : 0) * kChunkCols;
+    const int b = ok ? it / npu : 0;
+    const int cs = (pu0 + (ok ? it - b * npu : 0)) * kChunkCols;
     const int base = (small && a.hb > kChunkCols) ? cs - cs % a.hb : cs;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
@@ -165,7 +188,9 @@ __device__ __forceinline__ void store4h(uint16_t* p, const float v[4]) {
   *reinterpret_cast<u32x2_t*>(p) = w;
 }
 
-// Stage z rows [0, batch) x columns [0, G4 * 256) of linear P in LDS.
+// Stage z rows [0, batch) x columns [pu0 * 256, (pu0 + npu) * 256) of linear
+// P in LDS (column pu0 * 256 at LDS column 0; the BIG variant stages whole
+// rows: pu0 = 0, npu = G4).
 // Blocks of 1024..4096 columns (d a multiple of 1024, so G4 * 256 == d) go
 // through `scr` one batch row at a time: H_256 inside every chunk (fp32),
 // then H_(hb/256) across the chunks of each block -- the stages in order of
@@ -173,15 +198,15 @@ __device__ __forceinline__ void store4h(uint16_t* p, const float v[4]) {
 // BIG: the kernel variant for blocks above 512 columns (the only one that
 // holds that path's registers); the others take blocks <= 512 only.
 template <bool ROT, bool BIG, int NPRE>
-__device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>& f, bool pre, uint16_t* zl, float* scr,
-                            int tid, int wave, int lane) {
-  const int nch = a.G4;
+__device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>& f, bool pre, int pu0, int npu,
+                            uint16_t* zl, float* scr, int tid, int wave, int lane) {
+  const int nch = npu;
   if constexpr (!ROT) {
     const int per_row = nch * kChunkCols / 8;
     for (int i = tid; i < a.batch * per_row; i += kLinThreads) {
       const int b = i / per_row, c8 = (i - b * per_row) * 8;
       *reinterpret_cast<u32x4_t*>(zl + b * a.zstride + c8) =
-          *(const TP_GLOBAL u32x4_t*)(P.x + (size_t)b * P.ldx + c8);
+          *(const TP_GLOBAL u32x4_t*)(P.x + (size_t)b * P.ldx + pu0 * kChunkCols + c8);
     }
     return;
   }
@@ -194,7 +219,7 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>
         if (it < a.batch * nch) {
           const int b = it / nch, ci = it - b * nch;
           float v[4];
-          lin_pre_product(a, f, k, ci * kChunkCols, v);
+          lin_pre_product(a, f, k, (pu0 + ci) * kChunkCols, v);
           lin_chunk_fwht(a, lane, v);
           store4h(zl + b * a.zstride + ci * kChunkCols + lane * 4, v);
         }
@@ -204,7 +229,7 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>
     for (int it = it0; it < a.batch * nch; it += kLinWaves) {
       const int b = it / nch, ci = it - b * nch;
       float v[4];
-      lin_rotate_chunk(a, P, b, ci * kChunkCols, lane, v);
+      lin_rotate_chunk(a, P, b, (pu0 + ci) * kChunkCols, lane, v);
       store4h(zl + b * a.zstride + ci * kChunkCols + lane * 4, v);
     }
     return;
@@ -286,8 +311,11 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>
 // MULTI: 2..4 linears (part of a group is found per tile group); otherwise
 // one linear, whose argument fields sit at fixed offsets and load at once.
 // BIG: Hadamard blocks of 1024..4096 columns (lin_stage_z).
-template <int KB, int NS, int SB, bool ROT, bool MULTI, bool BIG>
+// KSPLIT: one linear, K cut into a.kparts parts (work item = tile group x
+// part); not with MULTI or BIG.
+template <int KB, int NS, int SB, bool ROT, bool MULTI, bool BIG, bool KSPLIT>
 __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a) {
+  static_assert(!(KSPLIT && (MULTI || BIG)), "K-split runs one linear with blocks <= 512");
   __shared__ __attribute__((aligned(16))) uint32_t table[kTableWords];
   extern __shared__ __attribute__((aligned(16))) char lin_lds[];
   constexpr int MW = member_words(KB);
@@ -310,6 +338,11 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     __asm__ volatile("" ::"s"(codebook), "s"(a.d), "s"(a.hb), "s"(a.batch), "s"(a.tpw), "s"(a.zstride),
                      "s"(a.hdiv), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(a.part[1].g0), "s"(a.part[2].g0),
                      "s"(a.part[3].g0)
+                     : "memory");
+  } else if constexpr (KSPLIT) {
+    const LinPart& P0 = a.part[0];
+    __asm__ volatile("" ::"s"(codebook), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(a.kparts), "s"(a.pu), "s"(P0.path),
+                     "s"(P0.member), "s"(P0.x), "s"(P0.rs)
                      : "memory");
   } else {
     const LinPart& P0 = a.part[0];
@@ -335,9 +368,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   const int bbz = bb < a.batch ? bb : 0;
   const int zrow = bbz * a.zstride + q * kSegCols;
   const int lt = wave / a.s;        // local tile of this wave
-  const int j = wave - lt * a.s;    // K chunk of this wave
-  const int u0 = j * a.c;
-  const int nu = min(a.c, a.G4 - u0);
+  const int j = wave - lt * a.s;    // K chunk of this wave (inside the K part)
   const uint32_t tile_p = (uint32_t)a.G4 * unit_p;  // path bytes of one tile
   const uint32_t tile_m = (uint32_t)a.G4 * unit_m;  // member bytes of one tile
   int staged = -1;
@@ -348,7 +379,17 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   // that its loads are scheduled from the kernel's entry state rather than
   // from the merged state of a loop: at the loop head the wait before the
   // weight loads also covered the activation prefetch.
-  auto group = [&](const int g) __attribute__((always_inline)) {
+  auto group = [&](const int w) __attribute__((always_inline)) {
+    // Work item w: tile group g, K part kp of units [pu0, pu0 + npu).
+    int g = w, kp = 0;
+    if constexpr (KSPLIT) {
+      g = w / a.kparts;
+      kp = w - g * a.kparts;
+    }
+    const int pu0 = KSPLIT ? kp * a.pu : 0;
+    const int npu = KSPLIT ? min(a.pu, a.G4 - pu0) : a.G4;
+    const int u0 = pu0 + j * a.c;
+    const int nu = min(a.c, pu0 + npu - u0);
     // The group's linear: the parts' first groups ascend and unused parts
     // start at `groups`, so it is the number of parts 1.. starting at or
     // before g.  (Computed from values of one argument round trip, then one
@@ -364,12 +405,13 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     const int t = (g - P.g0) * a.tpw + lt;
     const bool active = lt < a.tpw && t < P.T && nu > 0;  // wave-uniform
     const int tt = active ? t : 0;
+    const int key = p + kLinMaxParts * kp;  // what the LDS z holds
     // The first group's activations load before its weights (they gate the
     // rotation, which every decode waits for).
-    const bool pre = ROT && p != staged && g == (int)blockIdx.x;
+    const bool pre = ROT && key != staged && w == (int)blockIdx.x;
     XPre<lin_pre(KB)> xf;
     if constexpr (ROT) {
-      if (pre) xf = lin_prefetch_x<lin_pre(KB)>(a, P, wave, lane);
+      if (pre) xf = lin_prefetch_x<lin_pre(KB)>(a, P, pu0, npu, wave, lane);
     }
 
     // Every weight load of this wave, then the halo word (path word 1 of
@@ -391,11 +433,11 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     // dword with row n: the epilogue reads that row again)
     const u32x2_t sc = __builtin_amdgcn_raw_buffer_load_b64(srs, (uint32_t)(tt * kTileRows + 4 * q) * 2u, 0, 0);
 
-    if (g == (int)blockIdx.x) build_pair_table_lanes<KB>(table, cb_lane, tid, kLinThreads);
-    if (p != staged) {
+    if (w == (int)blockIdx.x) build_pair_table_lanes<KB>(table, cb_lane, tid, kLinThreads);
+    if (key != staged) {
       if (staged >= 0) __syncthreads();  // the previous group's reads of z and scr are done
-      lin_stage_z<ROT, BIG, lin_pre(KB)>(a, P, xf, pre, zl, scr, tid, wave, lane);
-      staged = p;
+      lin_stage_z<ROT, BIG, lin_pre(KB)>(a, P, xf, pre, pu0, npu, zl, scr, tid, wave, lane);
+      staged = key;
     }
     __syncthreads();
 
@@ -407,7 +449,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
 #pragma unroll
       for (int u = 0; u < kLinMaxUnits; ++u) {
         if (u < nu) {
-          const int cbase = (u0 + u) * kChunkCols;
+          const int cbase = (u0 + u - pu0) * kChunkCols;
 #pragma unroll
           for (int l = 0; l < NZ; ++l)
             R[u].Z[l] = *reinterpret_cast<const u32x4_t*>(zl + zrow + mfma_col(l * SLOTS + slot) + cbase);
@@ -433,12 +475,77 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     __syncthreads();
     if (active && j == 0) {
       float4_t v = *reinterpret_cast<const float4_t*>(scr + (wave * 64 + lane) * 4);
-      for (int k = 1; k < a.s; ++k) {
-        const float4_t w = *reinterpret_cast<const float4_t*>(scr + ((wave + k) * 64 + lane) * 4);
+      // (chunks of this part that hold units: a short last part has fewer)
+      const int sk = KSPLIT ? (npu + a.c - 1) / a.c : a.s;
+      for (int k = 1; k < sk; ++k) {
+        const float4_t o = *reinterpret_cast<const float4_t*>(scr + ((wave + k) * 64 + lane) * 4);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] += w[i];
+        for (int i = 0; i < 4; ++i) v[i] += o[i];
       }
-      if (slot == 0 && bb < a.batch) {
+      bool finish = true;
+      if constexpr (KSPLIT) {
+        if (a.kparts > 1) {
+          // This part's sums into its slice with coherent (L2-bypassing)
+          // stores, then the tile's counter.  Lanes of slot 0 hold the
+          // valid columns: rows 4q..4q+3 of batch column bb.
+          float* own = a.kws + ((size_t)kp * P.T + t) * kLinSliceFloats;
+          if (slot == 0 && bb < a.batch) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              __hip_atomic_store(own + (4 * q + i) * 8 + bb, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+          uint32_t old = 0;
+          if (lane == 0) old = __hip_atomic_fetch_add(a.kcnt + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          old = (uint32_t)__builtin_amdgcn_readfirstlane((int)old);
+          if (old + 1u == (uint32_t)a.kparts) {  // (wave-uniform) the last part of this tile
+            // Every lane owns entries (row, column) = (e / batch, e % batch),
+            // e = lane and lane + 64: all parts' values are loaded (coherent
+            // loads, all in flight at once) and added in part order, then
+            // the slices and the counter are left zero for the next call.
+            const int ne = kTileRows * a.batch;
+            const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(P.scales, (uint32_t)P.n * 2u);
+            // (buffer accesses over the kparts slices: a part past kparts is
+            // out of range, reads 0 and drops its store, with no branch;
+            // cache policy sc1, as the coherent stores and loads above)
+            const __amdgpu_buffer_rsrc_t krs =
+                buffer_rsrc(a.kws, (uint32_t)(a.kparts * P.T * kLinSliceFloats) * 4u);
+            const uint32_t pstride = (uint32_t)P.T * kLinSliceFloats * 4u;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+              const int e = lane + 64 * h;
+              if (e < ne) {
+                const int row = e / a.batch, col = e - row * a.batch;
+                const int grow = t * kTileRows + row;
+                const uint32_t off = ((uint32_t)t * kLinSliceFloats + (uint32_t)(row * 8 + col)) * 4u;
+                const uint16_t sv = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
+                    srs, grow < P.n ? (uint32_t)grow * 2u : kOutOfRange, 0, 0);
+                float part[kLinMaxKParts];
+#pragma unroll
+                for (int pp = 0; pp < kLinMaxKParts; ++pp)
+                  part[pp] = __builtin_bit_cast(
+                      float, __builtin_amdgcn_raw_buffer_load_b32(krs, off + (uint32_t)pp * pstride, 0, kCoherent));
+                float sum = part[0];
+#pragma unroll
+                for (int pp = 1; pp < kLinMaxKParts; ++pp)
+                  if (pp < a.kparts) sum += part[pp];
+                __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int pp = 0; pp < kLinMaxKParts; ++pp)
+                  __builtin_amdgcn_raw_buffer_store_b32(0u, krs, off + (uint32_t)pp * pstride, 0, kCoherent);
+                if (grow < P.n) {
+                  uint16_t out = f2h(sum * h2f(sv));
+                  if (P.bias) out = f2h(h2f(out) + h2f(gld(P.bias + grow)));
+                  gst(P.y + (size_t)col * P.ldy + grow, out);
+                }
+              }
+            }
+            if (lane == 0) __hip_atomic_store(a.kcnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          finish = false;  // (y written above, by the last part only)
+        }
+      }
+      if (finish && slot == 0 && bb < a.batch) {
         const int row0 = t * kTileRows + 4 * q;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -453,8 +560,9 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
       }
     }
   };
+  const int items = KSPLIT ? a.groups * a.kparts : a.groups;
   group((int)blockIdx.x);
-  for (int g = (int)(blockIdx.x + gridDim.x); g < a.groups; g += (int)gridDim.x) group(g);
+  for (int w = (int)(blockIdx.x + gridDim.x); w < items; w += (int)gridDim.x) group(w);
 }
 
 // ---------------------------------------------------------------------------
@@ -465,12 +573,14 @@ namespace {
 template <int KB, int NS, int SB, bool ROT>
 void launch_linear(const LinArgs& a, int grid, size_t dyn, hipStream_t s) {
   // (blocks above 512 columns run their own variant, so that the others
-  // keep that path's registers free: no spill frame, no scratch set-up)
+  // keep that path's registers free: no spill frame, no scratch set-up; the
+  // K-split variant is a third one)
   const bool big = ROT && a.hb > 2 * kChunkCols;
-  auto kern = big ? (a.n_part > 1 ? tcq_linear_kernel<KB, NS, SB, ROT, true, ROT>
-                                  : tcq_linear_kernel<KB, NS, SB, ROT, false, ROT>)
-                  : (a.n_part > 1 ? tcq_linear_kernel<KB, NS, SB, ROT, true, false>
-                                  : tcq_linear_kernel<KB, NS, SB, ROT, false, false>);
+  auto kern = big ? (a.n_part > 1 ? tcq_linear_kernel<KB, NS, SB, ROT, true, ROT, false>
+                                  : tcq_linear_kernel<KB, NS, SB, ROT, false, ROT, false>)
+                  : (a.n_part > 1 ? tcq_linear_kernel<KB, NS, SB, ROT, true, false, false>
+                     : a.kparts > 1 ? tcq_linear_kernel<KB, NS, SB, ROT, false, false, true>
+                                    : tcq_linear_kernel<KB, NS, SB, ROT, false, false, false>);
   allow_dynamic_lds(reinterpret_cast<const void*>(kern), kTableBytes + 256);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kLinThreads), dyn, s, a);
 }
@@ -483,10 +593,23 @@ void launch_linear_sb(const LinArgs& a, int grid, size_t dyn, bool rot, hipStrea
     rot ? launch_linear<KB, NS, 8, true>(a, grid, dyn, s) : launch_linear<KB, NS, 8, false>(a, grid, dyn, s);
 }
 
+// One way to cut a linear's work over the chip: K in kparts parts of pu
+// units, each part's K range in chunks of c units (sc chunks per tile), tpw
+// tiles per group of 16 waves.
+struct LinPlan {
+  int64_t kparts, pu, c, sc, tpw, groups, items;
+  double cost;
+};
+
 }  // namespace
 
+int64_t linear_ksplit_bytes(int64_t T) {
+  const int64_t tp = std::min<int64_t>(T * kLinMaxKParts, kLinMaxTileParts);
+  return tp * kLinSliceFloats * 4 + T * 4;
+}
+
 int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
-                        int bits, int n_states, hipStream_t s) {
+                        int bits, int n_states, hipStream_t s, bool clear_ws) {
   if (batch < 1 || batch > 8 || n_lin < 1 || n_lin > kLinMaxParts) return kLinearNotHandled;
   if (bits < 2 || bits > 4) return kLinearNotHandled;
   const bool rot = ls[0].rot_scale != nullptr;
@@ -498,29 +621,9 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   Geom g0;
   if (tiled_geom(ls[0].n, d, bits, &g0) != TP_OK) return kLinearNotHandled;
   const int64_t G4 = g0.G4;
-  if (G4 > (int64_t)kLinWaves * kLinMaxUnits) return kLinearNotHandled;
   if (rot && hb > 2 * kChunkCols && G4 * kChunkCols != d) return kLinearNotHandled;
-  // Staging issues the activations of lin_pre(bits) items per wave ahead
-  // of the weights; each further item costs a dependent round trip.  Blocks
-  // <= 512 columns take up to 6 items per wave (batch * 256-column chunks)
-  // before the split-K kernel is the faster one (Qwen3-4B down_proj, k=3,
-  // batch 2: 4.75 items, 17.3 -> 14.3 us).  Larger blocks stage one batch
-  // row at a time through LDS: up to 3 items per wave, batch <= 4 (o_proj,
-  // 4096-column blocks, batch 4 at 4 items: 18.0 -> 19.6 us).
   const bool rows8 = batch > 4;
   const bool big = rot && hb > 2 * kChunkCols;
-  if (rows8 && big) return kLinearNotHandled;
-  if (batch * G4 > (int64_t)kLinWaves * (big ? kLinPre + 1 : 6)) return kLinearNotHandled;
-
-  // LDS: 64 KiB table (static) + z rows + max(partial sums, one fp32 row).
-  const int64_t zstride = G4 * kChunkCols + 8;
-  const int64_t scr = std::max<int64_t>(kLinRedBytes, (rot && hb > 2 * kChunkCols) ? d * 4 : 0);
-  const int64_t room = (int64_t)device_max_lds() - kTableBytes - scr - 16;
-  const int64_t rows_fit = room > 0 ? room / (zstride * 2) : 0;
-  if (rows_fit < batch) return kLinearNotHandled;  // one launch for all rows (no weight re-reads)
-
-  // Split of each tile's K range: chunks of c units, s chunks per tile, tpw
-  // tiles per group of 16 waves; c grows until the groups fit one per CU.
   int64_t T[kLinMaxParts];
   for (int i = 0; i < n_lin; ++i) {
     Geom g;
@@ -528,33 +631,99 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
     T[i] = g.T;
   }
   const int cus = device_cu_count();
-  int64_t c = (G4 + kLinWaves - 1) / kLinWaves, sc = 0, tpw = 0, groups = 0;
-  for (;; ++c) {
-    sc = (G4 + c - 1) / c;
-    tpw = kLinWaves / sc;
-    groups = 0;
-    for (int i = 0; i < n_lin; ++i) groups += (T[i] + tpw - 1) / tpw;
-    if (groups <= cus || c >= kLinMaxUnits) break;
+  const int64_t lds_room = (int64_t)device_max_lds() - kTableBytes - 16;
+
+  // Candidate cuts, priced in us of a latency-bound launch: 1 per unit
+  // decoded per wave, 1.3 per staging item per wave among the first
+  // lin_pre(bits) (their activations load before the weights), 1.85 per
+  // later item (an activation round trip and a rotation chain), and for a
+  // K split 1.55 + 0.3 per part (the pass through memory: coherent stores,
+  // the tile's counter, the last part's loads), times the rounds when the
+  // groups outnumber the CUs.  (Least-squares fit to 21 forced cuts of
+  // Qwen3-4B gate_proj and down_proj, k=3, batch 1 / 4 / 8, on one box:
+  // e.g. down_proj batch 4: one part 17.1 us, 3 / 5 / 7 / 10 parts 14.1 /
+  // 12.0 / 11.9 / 12.5 us; gate_proj batch 1: one part 8.3 us, 2 / 3 parts
+  // 9.6 / 10.1 us.)
+  //
+  // Single part (the whole K range per workgroup): staging issues the
+  // activations of lin_pre(bits) items per wave ahead of the weights.
+  // Blocks <= 512 columns take up to 6 items per wave before the split-K
+  // kernel is the faster one (Qwen3-4B down_proj, k=3, batch 2: 4.75 items,
+  // 17.3 -> 14.3 us); larger blocks stage one batch row at a time through
+  // LDS: up to 3 items per wave, batch <= 4 (o_proj, 4096-column blocks,
+  // batch 4 at 4 items: 18.0 -> 19.6 us).  At batch 5..8 a single part
+  // pays off when each workgroup covers several row tiles (gate_proj k=3:
+  // 14.2 -> 11.8 us at batch 5, 15.6 -> 14.8 us at batch 8), not with one
+  // tile per workgroup (k_proj at batch 8: 10.3 -> 13.3 us).
+  //
+  // K parts (one linear, blocks <= 512, a workspace for the slices): each
+  // part covers whole Hadamard blocks, so a workgroup rotates its own part
+  // of the input; every (tile group, part) gets a CU of its own.
+  LinPlan best{0, 0, 0, 0, 0, 0, 0, 1e30};
+  const int64_t align = (rot && hb > kChunkCols) ? hb / kChunkCols : 1;  // units per Hadamard block
+  const bool can_split = n_lin == 1 && !big && ls[0].workspace && !((uintptr_t)ls[0].workspace & 15);
+  int64_t last_kparts = 0;
+  for (int64_t want = 1; want <= kLinMaxKParts && want <= G4; ++want) {
+    int64_t pu = (G4 + want - 1) / want;
+    pu = (pu + align - 1) / align * align;
+    const int64_t kparts = (G4 + pu - 1) / pu;
+    if (kparts == last_kparts) continue;
+    last_kparts = kparts;
+    if (kparts > 1) {
+      if (!can_split || kparts * T[0] > kLinMaxTileParts) continue;
+      if (ls[0].workspace_bytes < kparts * T[0] * kLinSliceFloats * 4 + T[0] * 4) continue;
+    }
+    // LDS: 64 KiB table (static) + z rows of the part + max(partial sums,
+    // one fp32 row); one launch stages every batch row (no weight re-reads)
+    const int64_t scr_bytes = std::max<int64_t>(kLinRedBytes, big ? d * 4 : 0);
+    if (lds_room - scr_bytes < batch * (pu * kChunkCols + 8) * 2) continue;
+    const int64_t items = (batch * pu + kLinWaves - 1) / kLinWaves;  // staging items per wave (blocks <= 512)
+    if (kparts == 1) {
+      if (pu > (int64_t)kLinWaves * kLinMaxUnits) continue;
+      if (batch * pu > (int64_t)kLinWaves * (big ? kLinPre + 1 : 6)) continue;
+      if (rows8 && big) continue;
+    } else if (items > 6) {
+      continue;
+    }
+    for (int64_t c = (pu + kLinWaves - 1) / kLinWaves; c <= kLinMaxUnits; ++c) {
+      const int64_t sc = (pu + c - 1) / c;
+      const int64_t tpw = kLinWaves / sc;
+      int64_t groups = 0;
+      for (int i = 0; i < n_lin; ++i) groups += (T[i] + tpw - 1) / tpw;
+      const int64_t wgs = groups * kparts;
+      if (wgs > cus && c < kLinMaxUnits) continue;  // one round if a larger c allows it
+      if (kparts == 1 && rows8 && tpw < 2) break;
+      if (groups > INT32_MAX / (2 * kLinMaxKParts)) break;
+      const int64_t pre = std::min<int64_t>(std::max<int64_t>(items, 1), lin_pre(bits));
+      const double stage = 1.3 * (double)pre + 1.85 * (double)std::max<int64_t>(items - pre, 0);
+      const double rounds = (double)((wgs + cus - 1) / cus);
+      const double split = kparts > 1 ? 1.55 + 0.3 * (double)kparts : 0.0;
+      const double cost = ((double)c + stage + split) * rounds;
+      if (cost < best.cost - 1e-9) best = LinPlan{kparts, pu, c, sc, tpw, groups, items, cost};
+      break;  // the smallest c that fits is the cheapest for this cut
+    }
   }
-  if (groups > INT32_MAX / 2) return kLinearNotHandled;
-  // At batch 5..8 every workgroup stages 5..8 input rows: that pays off when
-  // it covers several row tiles (Qwen3-4B gate_proj, k=3: 14.2 -> 11.8 us at
-  // batch 5, 15.6 -> 14.8 us at batch 8), not with one tile per workgroup
-  // (k_proj at batch 8: 10.3 -> 13.3 us).
-  if (rows8 && tpw < 2) return kLinearNotHandled;
+  if (best.kparts == 0) return kLinearNotHandled;
+
+  const int64_t zstride = best.pu * kChunkCols + 8;
+  const int64_t scr = std::max<int64_t>(kLinRedBytes, big ? d * 4 : 0);
 
   LinArgs a;
   a.codebook = codebook;
   a.n_part = n_lin;
-  a.groups = (int32_t)groups;
+  a.groups = (int32_t)best.groups;
   a.d = (int32_t)d;
   a.G4 = (int32_t)G4;
   a.hb = (int32_t)hb;
-  a.c = (int32_t)c;
-  a.s = (int32_t)sc;
-  a.tpw = (int32_t)tpw;
+  a.c = (int32_t)best.c;
+  a.s = (int32_t)best.sc;
+  a.tpw = (int32_t)best.tpw;
   a.zstride = (int32_t)zstride;
   a.hdiv = (float)__builtin_sqrt((double)hb);
+  a.kparts = (int32_t)best.kparts;
+  a.pu = (int32_t)best.pu;
+  a.kws = nullptr;
+  a.kcnt = nullptr;
   int64_t g0acc = 0;
   for (int i = 0; i < kLinMaxParts; ++i) {
     const TiledLinearArgs& l = ls[i < n_lin ? i : 0];
@@ -568,11 +737,21 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
     P.T = (int32_t)T[i < n_lin ? i : 0];
     P.ldx = (int32_t)l.ldx;
     P.ldy = (int32_t)l.ldy;
-    P.g0 = (int32_t)(i < n_lin ? g0acc : groups);
+    P.g0 = (int32_t)(i < n_lin ? g0acc : best.groups);
     P.reserved = 0;
-    if (i < n_lin) g0acc += (T[i] + tpw - 1) / tpw;
+    if (i < n_lin) g0acc += (T[i] + best.tpw - 1) / best.tpw;
   }
-  const int grid = (int)std::min<int64_t>(groups, cus);
+  if (best.kparts > 1) {
+    const int64_t slices = best.kparts * T[0] * kLinSliceFloats * 4;
+    a.kws = reinterpret_cast<float*>(ls[0].workspace);
+    a.kcnt = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(ls[0].workspace) + slices);
+    if (clear_ws) {
+      const int st = zero_device_bytes(ls[0].workspace, slices + T[0] * 4, s);
+      if (st) return st;
+    }
+  }
+  const int64_t work = best.groups * best.kparts;
+  const int grid = (int)std::min<int64_t>(work, cus);
   a.batch = (int32_t)batch;
   for (int i = 0; i < kLinMaxParts; ++i) {
     const TiledLinearArgs& l = ls[i < n_lin ? i : 0];

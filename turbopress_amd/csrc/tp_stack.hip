@@ -181,9 +181,9 @@ struct StackRO {  // views into the read-only part
   const int32_t* prefix;   // [n_lin + 1] first block of each linear
   const int32_t* lphase;   // [n_lin]
   const int32_t* pblocks;  // [n_phases] blocks per phase
-  const int32_t* sched_o;  // [total] (linear << 20) | block, phase order
+  const int32_t* sched_o;  // [total] (linear << kStackBlockBits) | block, phase order
   const int32_t* sched_u;  // [total] same blocks, longest K first
-  const int32_t* sched_wo; // [total_wide] (linear << 20) | wide block, phase order
+  const int32_t* sched_wo; // [total_wide] (linear << kStackBlockBits) | wide block, phase order
   const int32_t* sched_wu; // [total_wide] same, longest K first
   const int32_t* ptiles;   // [n_phases] row tiles per phase
   const OrdBlockDesc* oblk;  // [total_k] ordered-kernel blocks, phase order
@@ -1857,7 +1857,11 @@ inline int stack_sizes(const tp_stack_linear* linears, int n_linears, int bits, 
   for (int i = 0; i < n_linears; ++i) {
     const tp_stack_linear& l = linears[i];
     if (l.phase < 0 || l.phase >= kStackMaxPhases) return TP_ERR_BAD_DIMS;
-    if (i > 0 && l.phase < linears[i - 1].phase) return TP_ERR_BAD_DIMS;  // phases ascend
+    // Phases start at 0 and rise by at most 1 along the list: a phase waits
+    // for the one before it only, so an empty phase in between would let the
+    // phase after it start before the phase before the gap ended.
+    if (i == 0 ? l.phase != 0 : (l.phase < linears[i - 1].phase || l.phase > linears[i - 1].phase + 1))
+      return TP_ERR_BAD_DIMS;
     if (l.phase + 1 > z.n_phases) z.n_phases = l.phase + 1;
     Geom g;
     const int st = tiled_geom(l.n, l.d, bits, &g);
@@ -2084,6 +2088,8 @@ extern "C" int tp_stack_run(void* plan, int64_t batch, const uint16_t* codebook,
   if (total_blocks < 1 || total_blocks > INT32_MAX) return TP_ERR_BAD_DIMS;
   if (bits < 2 || bits > 4) return TP_ERR_UNSUPPORTED_BITS;
   if (n_states != 4 && n_states != 8 && n_states != 16 && n_states != 64) return TP_ERR_UNSUPPORTED_STATES;
+  // (every check of tp_stack_gemv before the rotation launch rewrites z)
+  if ((uintptr_t)codebook & 3) return TP_ERR_MISALIGNED;
   const int st = tp_stack_rotate(plan, batch, stream);
   if (st) return st;
   return tp_stack_gemv(plan, batch, codebook, bits, n_states, ordered, total_blocks, stream);

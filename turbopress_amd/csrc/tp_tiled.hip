@@ -32,6 +32,8 @@
 // The row scale is applied once at the end (turbopress/triton_kernel.py:70-73,123).
 #include "tp_tiled_common.h"
 
+#include <algorithm>
+
 namespace tp {
 
 struct GemvArgs {
@@ -392,7 +394,9 @@ extern "C" int64_t tp_gemv_workspace_bytes(int64_t n, int64_t batch) {
   if (n <= 0 || n > ((int64_t)1 << 30) || batch <= 0 || batch > 32) return 0;
   const int64_t T = (n + kTileRows - 1) / kTileRows;
   const int64_t nbt = batch <= 16 ? 1 : 2;
-  return T * kTileRows * 16 * nbt * 4 + T * 4;
+  // split-K sums + counters of the batch 5..32 kernels, or the K-split
+  // one-pass kernel's part slices + counters, whichever is larger
+  return std::max<int64_t>(T * kTileRows * 16 * nbt * 4 + T * 4, linear_ksplit_bytes(T));
 }
 
 extern "C" int tp_decode_tiled(const uint8_t* path_tiled, const uint8_t* member_tiled,
@@ -453,8 +457,13 @@ void launch_gemv_kb(const GemvArgs& a, int grid, int nbt, bool rot, hipStream_t 
   }
 }
 
+// clear_ws: the caller's workspaces may hold anything (the no-allocation
+// entry point's shared array): each launch that uses one is preceded by a
+// fill of the bytes it uses.  Otherwise workspaces are zero between calls,
+// which every kernel restores.  A workspace too small for the split-K kernel
+// is an error only when that kernel is the one that runs.
 int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
-                     int bits, int n_states, void* stream) {
+                     int bits, int n_states, void* stream, bool clear_ws) {
   if (n_lin < 1 || n_lin > kMaxInlineLinears) return TP_ERR_BAD_DIMS;
   if (!codebook) return TP_ERR_NULL_POINTER;
   if (bits < 2 || bits > 4) return TP_ERR_UNSUPPORTED_BITS;
@@ -479,6 +488,8 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
   if (kg < 1) kg = 1;
   if (kg > kMaxUnitsPerBlock) kg = kMaxUnitsPerBlock;
   int64_t total_blocks = 0;
+  int ws_status = TP_OK;           // the split-K kernel's workspace check, reported if it runs
+  int64_t ws_need[kMaxInlineLinears] = {0, 0, 0, 0};
   for (int i = 0; i < n_lin; ++i) {
     const TiledLinearArgs& l = ls[i];
     if (!l.path_tiled || !l.member_tiled || !l.x || !l.scales || !l.y) return TP_ERR_NULL_POINTER;
@@ -520,8 +531,12 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
     L.blocks = (int32_t)blocks;
     if (nkb > 1) {
       const int64_t need = g.T * kTileRows * 16 * nbt * 4 + g.T * 4;
-      if (!l.workspace || l.workspace_bytes < need) return TP_ERR_WORKSPACE;
-      if ((uintptr_t)l.workspace & 15) return TP_ERR_MISALIGNED;
+      if (!l.workspace || l.workspace_bytes < need) {
+        if (!ws_status) ws_status = TP_ERR_WORKSPACE;
+      } else if ((uintptr_t)l.workspace & 15) {
+        if (!ws_status) ws_status = TP_ERR_MISALIGNED;
+      }
+      ws_need[i] = need;
       L.ws = reinterpret_cast<float*>(l.workspace);
       L.cnt = reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(l.workspace) + g.T * kTileRows * 16 * nbt * 4);
     } else {
@@ -533,7 +548,7 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
   for (int i = n_lin; i < kMaxInlineLinears; ++i) a.lin[i] = a.lin[0];
   if (total_blocks > INT32_MAX) return TP_ERR_BAD_DIMS;
   // Batch <= 8 runs the one-pass kernel (tp_linear.hip) when it applies.
-  const int fast = linear_forward_fast(ls, n_lin, batch, codebook, bits, n_states, (hipStream_t)stream);
+  const int fast = linear_forward_fast(ls, n_lin, batch, codebook, bits, n_states, (hipStream_t)stream, clear_ws);
   if (fast != kLinearNotHandled) return fast;
   // Batch 9..32: 16-tile blocks through LDS (tp_stack.hip), on rotated
   // activations or rotating them in the launch (blocks <= 512).
@@ -544,11 +559,27 @@ int gemv_tiled_group(const TiledLinearArgs* ls, int n_lin, int64_t batch, const 
              !((uintptr_t)a.lin[i].x & 15) && !((uintptr_t)a.lin[i].rs & 15);
     if (wide) {
       for (int i = 0; i < n_lin; ++i) {
+        if (clear_ws && ls[i].workspace && !((uintptr_t)ls[i].workspace & 15)) {
+          // (the bytes the wide kernel uses when the workspace holds them)
+          const int64_t wneed = (int64_t)a.lin[i].T * kTileRows * 16 * nbt * 4 + (int64_t)a.lin[i].T * 4;
+          if (ls[i].workspace_bytes >= wneed) {
+            const int zst = zero_device_bytes(ls[i].workspace, wneed, (hipStream_t)stream);
+            if (zst) return zst;
+          }
+        }
         const int st = linear_forward_wide(a.lin[i], rot ? nullptr : ls[i].x, ls[i].ldx, batch, codebook, bits,
                                            n_states, ls[i].workspace, ls[i].workspace_bytes, (hipStream_t)stream);
         if (st) return st;
       }
       return TP_OK;
+    }
+  }
+  if (ws_status) return ws_status;
+  if (clear_ws) {
+    for (int i = 0; i < n_lin; ++i) {
+      if (!ws_need[i]) continue;
+      const int zst = zero_device_bytes(ls[i].workspace, ws_need[i], (hipStream_t)stream);
+      if (zst) return zst;
     }
   }
   a.total_blocks = (int32_t)total_blocks;
@@ -583,7 +614,7 @@ extern "C" int tp_tcq_gemv_tiled(const uint16_t* z, int64_t ldz, int64_t batch,
                                  void* stream) {
   TiledLinearArgs l{path_tiled, member_tiled, z, ldz, nullptr, 0, scales, bias, y, ldy, n, d,
                     workspace, workspace_bytes};
-  return gemv_tiled_group(&l, 1, batch, codebook, bits, n_states, stream);
+  return gemv_tiled_group(&l, 1, batch, codebook, bits, n_states, stream, false);
 }
 
 extern "C" int tp_packed_linear_forward(const uint16_t* x, int64_t ldx, int64_t batch,
@@ -596,8 +627,21 @@ extern "C" int tp_packed_linear_forward(const uint16_t* x, int64_t ldx, int64_t 
   if (!rot_scale) return TP_ERR_NULL_POINTER;
   TiledLinearArgs l{path_tiled, member_tiled, x, ldx, rot_scale, block, scales, bias, y, ldy, n, d,
                     workspace, workspace_bytes};
-  return gemv_tiled_group(&l, 1, batch, codebook, bits, n_states, stream);
+  return gemv_tiled_group(&l, 1, batch, codebook, bits, n_states, stream, false);
 }
+
+namespace tp {
+int packed_linear_forward_cleared(const uint16_t* x, int64_t ldx, int64_t batch, const uint16_t* rot_scale,
+                                  int64_t block, const uint8_t* path_tiled, const uint8_t* member_tiled,
+                                  const uint16_t* scales, const uint16_t* codebook, const uint16_t* bias, int64_t n,
+                                  int64_t d, int bits, int n_states, uint16_t* y, int64_t ldy, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+  if (!rot_scale) return TP_ERR_NULL_POINTER;
+  TiledLinearArgs l{path_tiled, member_tiled, x, ldx, rot_scale, block, scales, bias, y, ldy, n, d,
+                    workspace, workspace_bytes};
+  return gemv_tiled_group(&l, 1, batch, codebook, bits, n_states, stream, true);
+}
+}  // namespace tp
 
 extern "C" int tp_packed_linear_forward_group(int n_linears, const uint16_t* x, int64_t ldx,
                                               int64_t batch, const uint16_t* const* rot_scales,
@@ -619,5 +663,5 @@ extern "C" int tp_packed_linear_forward_group(int n_linears, const uint16_t* x, 
                             scales[i], biases ? biases[i] : nullptr, ys[i], ldys[i], ns[i], d,
                             workspaces[i], workspace_bytes[i]};
   }
-  return gemv_tiled_group(ls, n_linears, batch, codebook, bits, n_states, stream);
+  return gemv_tiled_group(ls, n_linears, batch, codebook, bits, n_states, stream, false);
 }

@@ -594,9 +594,26 @@ struct TiledLinearArgs {
 // Batch <= 8 decode-GEMV of 1..4 linears on one input in one pass
 // (tp_linear.hip), for arguments the caller has validated.  Returns a status,
 // or kLinearNotHandled when the shapes need the split-K kernel instead.
+// With one linear, Hadamard blocks <= 512 columns and a workspace, the K
+// range may also be cut into parts summed through the workspace (at most
+// linear_ksplit_bytes(T) of it, left zero); clear_ws zeroes that region
+// before the launch (for callers whose workspace may hold anything).
 constexpr int kLinearNotHandled = 1 << 20;
 int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
-                        int bits, int n_states, hipStream_t s);
+                        int bits, int n_states, hipStream_t s, bool clear_ws);
+int64_t linear_ksplit_bytes(int64_t T);
+
+// Zero `bytes` (a multiple of 4) of device memory with a fill kernel on
+// stream s (a kernel node rather than a memset node under graph capture).
+int zero_device_bytes(void* p, int64_t bytes, hipStream_t s);
+
+// tp_packed_linear_forward on a workspace that may hold anything: every
+// launch that uses it is preceded by a fill of the bytes it uses.
+int packed_linear_forward_cleared(const uint16_t* x, int64_t ldx, int64_t batch, const uint16_t* rot_scale,
+                                  int64_t block, const uint8_t* path_tiled, const uint8_t* member_tiled,
+                                  const uint16_t* scales, const uint16_t* codebook, const uint16_t* bias, int64_t n,
+                                  int64_t d, int bits, int n_states, uint16_t* y, int64_t ldy, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
 
 // Batch 9..32 decode-GEMV of one linear, in 16-tile blocks, K split across
 // workgroups through the workspace (tp_gemv_workspace_bytes) when one is

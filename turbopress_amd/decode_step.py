@@ -13,6 +13,11 @@ scripts/graph_decode_bench.py:70-118).  Two MI355X executors:
   * ``layer_forward`` -- one fused launch per group of linears sharing an
     input (q/k/v together, o, gate/up together, down): the launch structure a
     model with interleaved attention/norm kernels uses.
+  * ``ChainedDecodeStep`` -- the same four launches per layer with the data
+    dependencies of a decode step: o reads q's output, gate/up read o's,
+    down reads gate's, and the next layer's q/k/v read down's (the order
+    scripts/graph_decode_bench.py:86-115 replays through the HF decoder,
+    without the attention and norm kernels between the projections).
 
 Inputs are fixed device buffers (write new activations into ``inputs[i]``
 before each run), outputs are fixed buffers ``outputs[i]``, so runs can be
@@ -29,7 +34,7 @@ from torch import Tensor
 from turbopress_amd import _lib
 from turbopress_amd import hip_kernel as hk
 
-__all__ = ["LinearStack", "layer_forward", "QWEN_PHASES"]
+__all__ = ["LinearStack", "layer_forward", "ChainedDecodeStep", "QWEN_PHASES"]
 
 # Phase of each projection inside one decoder layer (shared-input groups).
 QWEN_PHASES = {"q_proj": 0, "k_proj": 0, "v_proj": 0, "o_proj": 1,
@@ -52,8 +57,8 @@ class LinearStack:
         self.linears = lins
         self.inputs = [e[1] for e in entries]
         self.phases = [int(e[2]) for e in entries]
-        if any(b < a for a, b in zip(self.phases, self.phases[1:])):
-            raise ValueError("phases must be non-decreasing along the stack")
+        if self.phases[0] != 0 or any(not a <= b <= a + 1 for a, b in zip(self.phases, self.phases[1:])):
+            raise ValueError("phases must start at 0 and rise by at most 1 along the stack")
         self.batch = int(self.inputs[0].shape[0])
         if not 1 <= self.batch <= 32:
             raise ValueError("stack batch must be in [1, 32]")
@@ -136,30 +141,89 @@ def layer_forward(mods: dict, xs: dict) -> dict:
     return out
 
 
+class ChainedDecodeStep:
+    """Decoder layers of packed linears run as a data-dependent chain.
+
+    ``layers`` is a list of dicts with the seven Qwen-style projections.  In
+    each layer ONE group launch runs q/k/v on the layer input, o runs on q's
+    output, ONE group launch runs gate/up on o's output, down runs on gate's
+    output, and down's output is the next layer's input: the Qwen3 shapes
+    chain exactly (2560 -> 4096 -> 2560 -> 9728 -> 2560 for Qwen3-4B).  k, v
+    and up are computed beside the chain, as in a decode step.  Four
+    launches per layer, each on the previous one's output, all on the
+    current stream with no host synchronisation, so a step can be captured
+    in a HIP graph: write the step's activations into ``input`` and replay;
+    ``outputs[i]`` holds layer i's seven projections of the last run (after
+    capture, tensors of the graph's memory pool that each replay rewrites).
+    """
+
+    def __init__(self, layers, input_buffer: Tensor) -> None:
+        if not layers:
+            raise ValueError("no layers")
+        for li, mods in enumerate(layers):
+            for a, b in (("q_proj", "o_proj"), ("o_proj", "gate_proj"), ("gate_proj", "down_proj")):
+                if mods[a].out_features != mods[b].in_features:
+                    raise ValueError(f"layer {li}: {a} output does not feed {b}")
+            if li + 1 < len(layers) and mods["down_proj"].out_features != layers[li + 1]["q_proj"].in_features:
+                raise ValueError(f"layer {li}: down_proj output does not feed the next layer")
+        if input_buffer.shape[-1] != layers[0]["q_proj"].in_features:
+            raise ValueError("input buffer does not match the first layer")
+        self.layers = layers
+        self.input = input_buffer
+        self.outputs: list = []
+
+    def run(self) -> Tensor:
+        """One decode step; returns the last layer's down_proj output."""
+        h = self.input
+        outs = []
+        for mods in self.layers:
+            q, k, v = hk.forward_group([mods["q_proj"], mods["k_proj"], mods["v_proj"]], h)
+            o = hk.forward_tiled(mods["o_proj"], q)
+            g, u = hk.forward_group([mods["gate_proj"], mods["up_proj"]], o)
+            h = hk.forward_tiled(mods["down_proj"], g)
+            outs.append({"q_proj": q, "k_proj": k, "v_proj": v, "o_proj": o, "gate_proj": g, "up_proj": u,
+                         "down_proj": h})
+        self.outputs = outs
+        return h
+
+    def layer_inputs(self, li: int) -> dict:
+        """The input each projection of layer li read in the last run."""
+        prev = self.input if li == 0 else self.outputs[li - 1]["down_proj"]
+        out = self.outputs[li]
+        return {"q_proj": prev, "k_proj": prev, "v_proj": prev, "o_proj": out["q_proj"],
+                "gate_proj": out["o_proj"], "up_proj": out["o_proj"], "down_proj": out["gate_proj"]}
+
+
 class SharedInputGroup:
     """Packed projections of one decoder layer that read the same input
-    (q/k/v, gate/up).  The first member called on an input runs ONE launch
-    for all of them (tp_packed_linear_forward_group) and keeps the other
-    outputs for the members' calls on that same input (same tensor storage,
-    version and shape); a member called on anything else runs the group
-    again; the held outputs are dropped once taken.  Outputs are those of
-    the members' own forwards (x's dtype)."""
+    (q/k/v, gate/up).  A member call runs ONE launch for all of them
+    (tp_packed_linear_forward_group) and holds the outputs of the members
+    after it in group order; a later member called on that same input (same
+    tensor storage, version and shape) takes its held output, once.  A call
+    of a member at or before the last one served starts a new pass and runs
+    the group again, dropping every held output, so a member skipped in one
+    step cannot hand its old output to the next step even when the input
+    buffer is rewritten in place under ``torch.inference_mode()`` (whose
+    tensors carry no version counter).  Decoders call the members in group
+    order each step (q, k, v; gate, up).  Outputs are those of the members'
+    own forwards (x's dtype)."""
 
     def __init__(self, members) -> None:
         self.members = list(members)
         self._key = None
+        self._last = -1
         self._pending = {}
 
     def run(self, index: int, x):
-        # (inference-mode tensors carry no version counter: storage, shape and
-        # strides then identify the input)
         version = None if x.is_inference() else x._version
         key = (x.data_ptr(), version, tuple(x.shape), tuple(x.stride()), x.dtype)
-        if key == self._key and index in self._pending:
+        if key == self._key and index > self._last and index in self._pending:
+            self._last = index
             return self._pending.pop(index)
         outs = [o.to(x.dtype) for o in hk.forward_group(self.members, x)]
         self._key = key
-        self._pending = {i: o for i, o in enumerate(outs) if i != index}
+        self._last = index
+        self._pending = {i: o for i, o in enumerate(outs) if i > index}
         return outs[index]
 
 

@@ -165,8 +165,68 @@ def retile(path_packed: Tensor, member_packed: Tensor, n: int, d: int, bits: int
 
 
 def gemv_workspace(n: int, batch: int, device) -> Tensor:
+    """A zeroed split-K workspace of its own for an n-row linear at `batch`
+    rows (tp_gemv_workspace_bytes)."""
     nbytes = int(_lib.lib().tp_gemv_workspace_bytes(n, batch))
     return torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
+def workspace_bytes(n: int) -> tuple:
+    """Split-K workspace bytes of an n-row linear at batch <= 16 and <= 32."""
+    lib = _lib.lib()
+    return int(lib.tp_gemv_workspace_bytes(n, 16)), int(lib.tp_gemv_workspace_bytes(n, 32))
+
+
+# One split-K workspace per (device, stream), shared by every packed linear
+# launched on that stream.  The kernels leave it zero when they finish, so
+# launches in stream order can share it; launches that overlap on one
+# workspace (two streams would need two) are not allowed, hence one per
+# stream.  A workspace that grows is replaced, and the old one stays alive:
+# a captured graph may still name it.
+_WORKSPACES: dict = {}
+_RETIRED_WORKSPACES: list = []
+_WS_ALIGN = 256
+
+
+def _aligned(nbytes: int) -> int:
+    return (nbytes + _WS_ALIGN - 1) // _WS_ALIGN * _WS_ALIGN
+
+
+def shared_workspace(device, nbytes: int) -> Tensor:
+    """The zeroed split-K workspace of `device` and its current stream, at
+    least `nbytes` long (allocated or grown on first need)."""
+    dev = torch.device(device)
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    key = (index, torch.cuda.current_stream(index).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED_WORKSPACES.append(ws)
+        ws = torch.zeros(max(_aligned(nbytes), _WS_ALIGN), dtype=torch.uint8,
+                         device=torch.device("cuda", index))
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def layer_workspace(layer, batch: int) -> tuple:
+    """(pointer, bytes) of the shared workspace for one launch of `layer` at
+    `batch` rows (<= 32)."""
+    need = layer._ws_bytes[0 if batch <= 16 else 1]
+    ws = shared_workspace(layer.tiled_packed.device, need)
+    return ws.data_ptr(), need
+
+
+def group_workspaces(layers, batch: int) -> tuple:
+    """Disjoint regions of the shared workspace for the linears of one group
+    launch (they run concurrently): lists of pointers and sizes."""
+    needs = [lyr._ws_bytes[0 if batch <= 16 else 1] for lyr in layers]
+    offs, total = [], 0
+    for need in needs:
+        offs.append(total)
+        total += _aligned(need)
+    ws = shared_workspace(layers[0].tiled_packed.device, total)
+    base = ws.data_ptr()
+    return [base + o for o in offs], needs
 
 
 def decode_tiled(layer) -> Tensor:
@@ -199,18 +259,18 @@ def gemv_tiled(zpad: Tensor, layer, bias: Tensor | None, out: Tensor) -> Tensor:
     """out[B, n] = packed GEMV over the device layout; zpad fp16 [B, ldz]."""
     n, d = layer.out_features, layer.in_features
     buf = layer.tiled_packed
-    ws = layer._gemv_ws
     pb = layer._tiled_geo["path_bytes"]
     ldz = zpad.shape[1]
     stream = current_stream_ptr(zpad.device)
     lib = _lib.lib()
     for b0 in range(0, zpad.shape[0], 32):
         nb = min(32, zpad.shape[0] - b0)
+        ws, ws_bytes = layer_workspace(layer, nb)
         st = lib.tp_tcq_gemv_tiled(
             zpad.data_ptr() + 2 * b0 * ldz, ldz, nb, buf.data_ptr(), buf.data_ptr() + pb,
             layer.scales.data_ptr(), layer.codebook.data_ptr(),
             0 if bias is None else bias.data_ptr(), n, d, layer.bits, layer.n_states,
-            out.data_ptr() + 2 * b0 * n, n, ws.data_ptr(), ws.numel(), stream)
+            out.data_ptr() + 2 * b0 * n, n, ws, ws_bytes, stream)
         _lib.check(st, "tcq_gemv_tiled")
     return out
 
@@ -231,18 +291,19 @@ def forward_tiled(layer, x: Tensor) -> Tensor:
         zpad = rotate_padded(flat, layer.rot_scale, layer.block, layer._tiled_geo["z_cols"])
         gemv_tiled(zpad, layer, layer.bias, y)
         return y.reshape(*x.shape[:-1], n)
-    buf, ws = layer.tiled_packed, layer._gemv_ws
+    buf = layer.tiled_packed
     pb = layer._tiled_geo["path_bytes"]
     bias = layer.bias
     stream = current_stream_ptr(x.device)
     lib = _lib.lib()
     for b0 in range(0, flat.shape[0], 32):
         nb = min(32, flat.shape[0] - b0)
+        ws, ws_bytes = layer_workspace(layer, nb)
         st = lib.tp_packed_linear_forward(
             flat.data_ptr() + 2 * b0 * d, d, nb, layer.rot_scale.data_ptr(), layer.block,
             buf.data_ptr(), buf.data_ptr() + pb, layer.scales.data_ptr(), layer.codebook.data_ptr(),
             0 if bias is None else bias.data_ptr(), n, d, layer.bits, layer.n_states,
-            y.data_ptr() + 2 * b0 * n, n, ws.data_ptr(), ws.numel(), stream)
+            y.data_ptr() + 2 * b0 * n, n, ws, ws_bytes, stream)
         _lib.check(st, "packed_linear_forward")
     return y.reshape(*x.shape[:-1], n)
 
@@ -274,6 +335,7 @@ def forward_group(layers, x: Tensor) -> list:
     lib = _lib.lib()
     for b0 in range(0, flat.shape[0], 32):
         nb = min(32, flat.shape[0] - b0)
+        ws_ptrs, ws_sizes = group_workspaces(layers, nb)
         st = lib.tp_packed_linear_forward_group(
             k, flat.data_ptr() + 2 * b0 * d, d, nb,
             P(*[lyr.rot_scale.data_ptr() for lyr in layers]), I(*[lyr.block for lyr in layers]),
@@ -283,7 +345,7 @@ def forward_group(layers, x: Tensor) -> list:
             P(*[0 if lyr.bias is None else lyr.bias.data_ptr() for lyr in layers]),
             I(*[lyr.out_features for lyr in layers]), d, l0.bits, l0.n_states,
             P(*[o.data_ptr() + 2 * b0 * o.shape[1] for o in outs]), I(*[o.shape[1] for o in outs]),
-            P(*[lyr._gemv_ws.data_ptr() for lyr in layers]), I(*[lyr._gemv_ws.numel() for lyr in layers]),
+            P(*ws_ptrs), I(*ws_sizes),
             stream)
         _lib.check(st, "packed_linear_forward_group")
     return [o.reshape(*x.shape[:-1], o.shape[1]) for o in outs]

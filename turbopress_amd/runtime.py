@@ -95,7 +95,11 @@ class PackedTCQLinear(nn.Module):
         self.bits: int = int(payload["bits"])
         self.n_states: int = int(payload["n_states"])
         self.block: int = int(payload["block"])
-        self.mode = "hip" if mode == "triton" else mode
+        # The mode string is kept as given (runtime.py:231): the reference's
+        # scripts check ``module.mode == "triton"`` (bench_packed.py:286-293).
+        # "triton" and "hip" select the same packed HIP path.
+        self.mode = mode
+        self._packed_path = mode in ("hip", "triton")
         self.tile_rows = tile_rows
         self._trellis = Trellis(self.n_states)
         dev = _target_device(payload)
@@ -131,11 +135,11 @@ class PackedTCQLinear(nn.Module):
         self.register_buffer("levels_packed", None)
 
         self.register_buffer("tiled_packed", None)
-        self.register_buffer("_gemv_ws", None, persistent=False)
         self._tiled_geo = None
+        self._ws_bytes = (0, 0)  # split-K workspace need at batch <= 16 / <= 32
         self._group = None       # SharedInputGroup this layer belongs to (decode_step)
         self._group_index = 0
-        if self.mode == "hip":
+        if self._packed_path:
             if self.bits in hk.TILED_BITS:
                 # Load-time re-tile into the MFMA kernel's layout, still at the
                 # true k bits/weight (the reference re-packs (k+1)-bit levels
@@ -143,7 +147,12 @@ class PackedTCQLinear(nn.Module):
                 self._tiled_geo = hk.tiled_layout(self.out_features, d, self.bits)
                 self.tiled_packed = hk.retile(self.path_packed, self.member_packed,
                                               self.out_features, d, self.bits)
-                self._gemv_ws = hk.gemv_workspace(self.out_features, 32, dev)
+                # The split-K workspace (batch 5..32 and some larger shapes)
+                # is not the layer's own: one zeroed buffer per device and
+                # stream is shared by every packed linear (hip_kernel.
+                # shared_workspace), where the reference allocates its fp32
+                # output per call (triton_kernel.py:141).
+                self._ws_bytes = hk.workspace_bytes(self.out_features)
                 for name in ("path_packed", "member_packed"):
                     setattr(self, name, None)
                 self.levels_packed = self.tiled_packed
@@ -200,7 +209,7 @@ class PackedTCQLinear(nn.Module):
         if self.tiled_packed is not None:
             return hk.forward_tiled(self, x).to(x.dtype)
         z = hk.fwht_scale(x, self.rot_scale, self.block)
-        if self.mode == "hip":
+        if self._packed_path:
             y = hk.packed_gemv(z, self, bias=self.bias)
         else:  # tiled
             flat = z.reshape(-1, self.in_features)

@@ -69,6 +69,22 @@ def _synthetic_codebook(bits: int, seed: int) -> torch.Tensor:
     return cb.to(torch.float16)
 
 
+def unit_gain(payload: dict) -> dict:
+    """The payload with its row scales divided by the linear's expected gain
+    sqrt(n * mean(scale^2) * mean(codebook^2) * mean(inv_equil^2)), so that
+    E||y||^2 = ||x||^2 for uniform codes: chains of such linears keep the
+    activations' magnitude (decode-step benchmarks without the model's
+    norms).  The codes, codebook and rotation are unchanged."""
+    out = dict(payload)
+    n = int(payload["n"])
+    s = payload["scales"].float()
+    cb = payload["codebook"].float()
+    ie = payload["inv_equil"].float()
+    gain = math.sqrt(n * float(s.pow(2).mean()) * float(cb.pow(2).mean()) * float(ie.pow(2).mean()))
+    out["scales"] = (s / gain).to(torch.float16)
+    return out
+
+
 def make_payload(n: int, d: int, bits: int, n_states: int = 64, seed: int = 0,
                  bias: bool = False, codebook: torch.Tensor | None = None) -> dict:
     """A seeded format-v2 payload of an n x d packed linear (CPU tensors)."""
