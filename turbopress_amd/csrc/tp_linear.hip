@@ -6,7 +6,8 @@
 // A single 9.4 MB linear has only ~1.5 units of work per wave of the chip, so
 // the launch is built around latency rather than streaming:
 //   * one workgroup of 16 waves per CU; the group owns `tpw` row tiles and
-//     splits each tile's K range into `s` chunks of at most 3 units, one
+//     splits each tile's K range into `s` chunks of at most 3 units (4
+//     when several linears share the launch), one
 //     chunk per wave, so every weight load of the launch is issued in the
 //     first few hundred cycles;
 //   * while those loads are in flight the workgroup builds the pair table
@@ -32,7 +33,15 @@ namespace tp {
 
 constexpr int kLinWaves = 16;
 constexpr int kLinThreads = 64 * kLinWaves;
-constexpr int kLinMaxUnits = 3;                      // units per wave, all loaded up front
+// Units per wave, all loaded up front: 3, and 4 in launches of several
+// linears, where it lets two 9728-row linears (gate/up sharing their input)
+// fit one round of 244 workgroups (3 units: 304 workgroups on 256 CUs, two
+// rounds; 17.0 -> 10.7 us at batch 1).  The single-linear variants keep 3:
+// a fourth register set of loads, issued out of range when unused, made
+// them ~0.3 us slower.
+constexpr int kLinMaxUnits = 3;
+constexpr int kLinMaxUnitsMulti = 4;
+__host__ __device__ constexpr int lin_max_units(bool multi) { return multi ? kLinMaxUnitsMulti : kLinMaxUnits; }
 constexpr int kLinMaxParts = kMaxInlineLinears;
 constexpr int kLinRedBytes = kLinWaves * 64 * 16;    // one float4 per lane and wave
 // K-split: a part's sums of one row tile are [16 rows][8 batch columns] fp32
@@ -418,9 +427,10 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     // the unit before the chunk, K block 3 lanes) and the row scales.
     const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(reinterpret_cast<const char*>(P.path) + (size_t)tt * tile_p, tile_p);
     const __amdgpu_buffer_rsrc_t mrs = buffer_rsrc(reinterpret_cast<const char*>(P.member) + (size_t)tt * tile_m, tile_m);
-    UnitRegs<MW, NZ> R[kLinMaxUnits];
+    constexpr int MAXU = lin_max_units(MULTI);
+    UnitRegs<MW, NZ> R[MAXU];
 #pragma unroll
-    for (int u = 0; u < kLinMaxUnits; ++u) {
+    for (int u = 0; u < MAXU; ++u) {
       const bool ok = active && u < nu;
       const uint32_t gu = (uint32_t)(ok ? u0 + u : 0);
       R[u].X = __builtin_amdgcn_raw_buffer_load_b64(prs, ok ? pv : kOutOfRange, gu * unit_p, weight_policy(MW));
@@ -447,7 +457,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
       for (int s = 0; s < SLOTS; ++s) acc[s] = float4_t{0.f, 0.f, 0.f, 0.f};
       uint32_t prev = x1_prev;
 #pragma unroll
-      for (int u = 0; u < kLinMaxUnits; ++u) {
+      for (int u = 0; u < MAXU; ++u) {
         if (u < nu) {
           const int cbase = (u0 + u - pu0) * kChunkCols;
 #pragma unroll
@@ -637,13 +647,15 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   // decoded per wave, 1.3 per staging item per wave among the first
   // lin_pre(bits) (their activations load before the weights), 1.85 per
   // later item (an activation round trip and a rotation chain), and for a
-  // K split 1.55 + 0.3 per part (the pass through memory: coherent stores,
+  // K split 2.3 + 0.3 per part (the pass through memory: coherent stores,
   // the tile's counter, the last part's loads), times the rounds when the
-  // groups outnumber the CUs.  (Least-squares fit to 21 forced cuts of
-  // Qwen3-4B gate_proj and down_proj, k=3, batch 1 / 4 / 8, on one box:
-  // e.g. down_proj batch 4: one part 17.1 us, 3 / 5 / 7 / 10 parts 14.1 /
-  // 12.0 / 11.9 / 12.5 us; gate_proj batch 1: one part 8.3 us, 2 / 3 parts
-  // 9.6 / 10.1 us.)
+  // groups outnumber the CUs.  (Fitted to 21 forced cuts of Qwen3-4B
+  // gate_proj and down_proj, k=3, batch 1 / 4 / 8, on one box -- e.g.
+  // down_proj batch 4: one part 17.1 us, 3 / 5 / 7 / 10 parts 14.1 / 12.0
+  // / 11.9 / 12.5 us; gate_proj batch 1: one part 8.3 us, 2 / 3 parts 9.6 /
+  // 10.1 us -- with the split's fixed cost raised from the fit's 1.55 to
+  // 2.3 so that gate_proj at batch 4 keeps one part: 10.3 us, 3 parts
+  // 10.6 us.)
   //
   // Single part (the whole K range per workgroup): staging issues the
   // activations of lin_pre(bits) items per wave ahead of the weights.
@@ -663,6 +675,7 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   const int64_t align = (rot && hb > kChunkCols) ? hb / kChunkCols : 1;  // units per Hadamard block
   const bool can_split = n_lin == 1 && !big && ls[0].workspace && !((uintptr_t)ls[0].workspace & 15);
   int64_t last_kparts = 0;
+  const int64_t maxu = lin_max_units(n_lin > 1);
   for (int64_t want = 1; want <= kLinMaxKParts && want <= G4; ++want) {
     int64_t pu = (G4 + want - 1) / want;
     pu = (pu + align - 1) / align * align;
@@ -679,25 +692,25 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
     if (lds_room - scr_bytes < batch * (pu * kChunkCols + 8) * 2) continue;
     const int64_t items = (batch * pu + kLinWaves - 1) / kLinWaves;  // staging items per wave (blocks <= 512)
     if (kparts == 1) {
-      if (pu > (int64_t)kLinWaves * kLinMaxUnits) continue;
+      if (pu > (int64_t)kLinWaves * maxu) continue;
       if (batch * pu > (int64_t)kLinWaves * (big ? kLinPre + 1 : 6)) continue;
       if (rows8 && big) continue;
     } else if (items > 6) {
       continue;
     }
-    for (int64_t c = (pu + kLinWaves - 1) / kLinWaves; c <= kLinMaxUnits; ++c) {
+    for (int64_t c = (pu + kLinWaves - 1) / kLinWaves; c <= maxu; ++c) {
       const int64_t sc = (pu + c - 1) / c;
       const int64_t tpw = kLinWaves / sc;
       int64_t groups = 0;
       for (int i = 0; i < n_lin; ++i) groups += (T[i] + tpw - 1) / tpw;
       const int64_t wgs = groups * kparts;
-      if (wgs > cus && c < kLinMaxUnits) continue;  // one round if a larger c allows it
+      if (wgs > cus && c < maxu) continue;  // one round if a larger c allows it
       if (kparts == 1 && rows8 && tpw < 2) break;
       if (groups > INT32_MAX / (2 * kLinMaxKParts)) break;
       const int64_t pre = std::min<int64_t>(std::max<int64_t>(items, 1), lin_pre(bits));
       const double stage = 1.3 * (double)pre + 1.85 * (double)std::max<int64_t>(items - pre, 0);
       const double rounds = (double)((wgs + cus - 1) / cus);
-      const double split = kparts > 1 ? 1.55 + 0.3 * (double)kparts : 0.0;
+      const double split = kparts > 1 ? 2.3 + 0.3 * (double)kparts : 0.0;
       const double cost = ((double)c + stage + split) * rounds;
       if (cost < best.cost - 1e-9) best = LinPlan{kparts, pu, c, sc, tpw, groups, items, cost};
       break;  // the smallest c that fits is the cheapest for this cut
