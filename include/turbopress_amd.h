@@ -211,6 +211,19 @@ int tp_packed_linear_forward_noalloc(const uint16_t* x, int64_t ldx, int64_t bat
                                      const uint16_t* bias, int64_t n, int64_t d, int bits,
                                      int n_states, uint16_t* y, int64_t ldy, void* stream);
 
+/* Host only: the cut the batch <= 8 one-pass kernel of
+ * tp_packed_linear_forward / tp_packed_linear_forward_group takes for
+ * n_linears linears of ns[i] rows sharing d columns (Hadamard block
+ * `block`), on a device of `cus` compute units and `lds_bytes` of LDS per
+ * workgroup, with a workspace of workspace_bytes (0: none).  out[0..5] =
+ * K parts (0: the kernel declines; the split-K kernel runs), 256-column
+ * units per part, units per wave, chunks per row tile, row tiles per
+ * workgroup, workgroups.  No reference counterpart: it reports the
+ * library's planning (tests and tuning). */
+int tp_linear_forward_plan(const int64_t* ns, int n_linears, int64_t d, int64_t block, int bits,
+                           int64_t batch, int64_t workspace_bytes, int cus, int64_t lds_bytes,
+                           int64_t* out);
+
 /* One launch for up to 4 packed linears that read the same input x (e.g. the
  * q/k/v or gate/up projections of a decoder layer) and share one codebook:
  * each has its own rot_scale/block, streams, scales, bias (array may be NULL),

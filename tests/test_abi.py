@@ -174,3 +174,38 @@ def test_device_code_indexes_no_register_arrays(tmp_path):
         assert "scratch_load" not in asm and "scratch_store" not in asm, name
         for kern, body in re.findall(r"\.amdhsa_kernel (\S+)\n(.*?)\.end_amdhsa_kernel", asm, re.S):
             assert ".amdhsa_enable_private_segment 1" not in body, (name, kern)
+
+
+def _plan(lib, ns, d, block, batch, bits=3, ws=1 << 21, cus=256, lds=160 * 1024):
+    arr = (ctypes.c_int64 * len(ns))(*ns)
+    out = (ctypes.c_int64 * 6)()
+    assert lib.tp_linear_forward_plan(arr, len(ns), d, block, bits, batch, ws, cus, lds, out) == 0
+    return dict(zip(("kparts", "units_per_part", "units_per_wave", "chunks", "tiles_per_group", "workgroups"),
+                    list(out)))
+
+
+def test_linear_planner_cuts_at_the_qwen3_4b_shapes(built_lib):
+    """The one-pass kernel's plan on a 256-CU, 160 KiB-LDS device (host only):
+    down_proj (2560 x 9728) cuts K into parts of whole 512-column Hadamard
+    blocks at batch 1..8 (many parts at batch 4 / 8, where one part would
+    stage the whole input in every workgroup); gate_proj keeps one part at
+    batch 1 and 4 and takes 3 at batch 8; the gate/up pair fits one round of
+    workgroups with 4 units per wave; o_proj's 4096-column block is never
+    split; without a workspace nothing is split; batch 9 is not this
+    kernel's."""
+    lib = built_lib
+    for batch in (1, 4, 8):
+        p = _plan(lib, [2560], 9728, 512, batch)
+        assert p["kparts"] >= 3 and p["units_per_part"] % 2 == 0, (batch, p)
+        assert p["workgroups"] <= 256 and p["units_per_part"] * p["kparts"] >= 38
+    assert _plan(lib, [2560], 9728, 512, 4)["kparts"] >= 5
+    assert _plan(lib, [9728], 2560, 512, 1) == {"kparts": 1, "units_per_part": 10, "units_per_wave": 2,
+                                                  "chunks": 5, "tiles_per_group": 3, "workgroups": 203}
+    assert _plan(lib, [9728], 2560, 512, 4)["kparts"] == 1
+    assert _plan(lib, [9728], 2560, 512, 8)["kparts"] == 3
+    pair = _plan(lib, [9728, 9728], 2560, 512, 1)
+    assert pair["kparts"] == 1 and pair["units_per_wave"] == 4 and pair["workgroups"] <= 256
+    o = _plan(lib, [2560], 4096, 4096, 1)
+    assert o["kparts"] == 1 and o["workgroups"] == 160
+    assert _plan(lib, [2560], 9728, 512, 4, ws=0)["kparts"] == 0  # no workspace: the split-K kernel
+    assert _plan(lib, [2560], 9728, 512, 9)["kparts"] == 0

@@ -45,6 +45,8 @@ SIGNATURES: dict[str, tuple] = {
                                 POINTER(c_int64), POINTER(c_int64), POINTER(c_int64)]),
     "tp_retile": (c_int, [_P, _I64, _P, _I64, _I64, _I64, c_int, _P, _P, _P]),
     "tp_gemv_workspace_bytes": (c_int64, [_I64, _I64]),
+    "tp_linear_forward_plan": (c_int, [POINTER(c_int64), c_int, _I64, _I64, c_int, _I64, _I64, c_int, _I64,
+                                       POINTER(c_int64)]),
     "tp_tcq_gemv_tiled": (c_int, [_P, _I64, _I64, _P, _P, _P, _P, _P, _I64, _I64, c_int, c_int,
                                   _P, _I64, _P, _I64, _P]),
     "tp_decode_tiled": (c_int, [_P, _P, _P, _P, _I64, _I64, c_int, c_int, _P, _I64, _P]),

@@ -618,31 +618,15 @@ int64_t linear_ksplit_bytes(int64_t T) {
   return tp * kLinSliceFloats * 4 + T * 4;
 }
 
-int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
-                        int bits, int n_states, hipStream_t s, bool clear_ws) {
-  if (batch < 1 || batch > 8 || n_lin < 1 || n_lin > kLinMaxParts) return kLinearNotHandled;
-  if (bits < 2 || bits > 4) return kLinearNotHandled;
-  const bool rot = ls[0].rot_scale != nullptr;
-  const int64_t d = ls[0].d, hb = rot ? ls[0].block : 1;
-  for (int i = 1; i < n_lin; ++i)
-    if (ls[i].d != d || (rot && ls[i].block != hb) || ls[i].x != ls[0].x || ls[i].ldx != ls[0].ldx)
-      return kLinearNotHandled;
-  if (rot && hb > 4096) return kLinearNotHandled;
-  Geom g0;
-  if (tiled_geom(ls[0].n, d, bits, &g0) != TP_OK) return kLinearNotHandled;
-  const int64_t G4 = g0.G4;
-  if (rot && hb > 2 * kChunkCols && G4 * kChunkCols != d) return kLinearNotHandled;
+// The cut of the one-pass kernel for n_lin linears of T[i] row tiles over
+// G4 units of K (Hadamard block hb when rot), or kparts == 0 when it
+// declines the shapes (the split-K kernel runs).  Host only, no device
+// state: cus and max_lds describe the device.
+LinPlan plan_linear(int n_lin, const int64_t* T, int64_t G4, int64_t d, int64_t hb, bool rot, int64_t batch,
+                    int bits, bool can_split, int64_t workspace_bytes, int cus, int64_t max_lds) {
   const bool rows8 = batch > 4;
   const bool big = rot && hb > 2 * kChunkCols;
-  int64_t T[kLinMaxParts];
-  for (int i = 0; i < n_lin; ++i) {
-    Geom g;
-    if (tiled_geom(ls[i].n, d, bits, &g) != TP_OK) return kLinearNotHandled;
-    T[i] = g.T;
-  }
-  const int cus = device_cu_count();
-  const int64_t lds_room = (int64_t)device_max_lds() - kTableBytes - 16;
-
+  const int64_t lds_room = max_lds - kTableBytes - 16;
   // Candidate cuts, priced in us of a latency-bound launch: 1 per unit
   // decoded per wave, 1.3 per staging item per wave among the first
   // lin_pre(bits) (their activations load before the weights), 1.85 per
@@ -673,7 +657,7 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   // of the input; every (tile group, part) gets a CU of its own.
   LinPlan best{0, 0, 0, 0, 0, 0, 0, 1e30};
   const int64_t align = (rot && hb > kChunkCols) ? hb / kChunkCols : 1;  // units per Hadamard block
-  const bool can_split = n_lin == 1 && !big && ls[0].workspace && !((uintptr_t)ls[0].workspace & 15);
+  can_split = can_split && n_lin == 1 && !big;
   int64_t last_kparts = 0;
   const int64_t maxu = lin_max_units(n_lin > 1);
   for (int64_t want = 1; want <= kLinMaxKParts && want <= G4; ++want) {
@@ -684,7 +668,7 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
     last_kparts = kparts;
     if (kparts > 1) {
       if (!can_split || kparts * T[0] > kLinMaxTileParts) continue;
-      if (ls[0].workspace_bytes < kparts * T[0] * kLinSliceFloats * 4 + T[0] * 4) continue;
+      if (workspace_bytes < kparts * T[0] * kLinSliceFloats * 4 + T[0] * 4) continue;
     }
     // LDS: 64 KiB table (static) + z rows of the part + max(partial sums,
     // one fp32 row); one launch stages every batch row (no weight re-reads)
@@ -716,6 +700,34 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
       break;  // the smallest c that fits is the cheapest for this cut
     }
   }
+  return best;
+}
+
+int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, const uint16_t* codebook,
+                        int bits, int n_states, hipStream_t s, bool clear_ws) {
+  if (batch < 1 || batch > 8 || n_lin < 1 || n_lin > kLinMaxParts) return kLinearNotHandled;
+  if (bits < 2 || bits > 4) return kLinearNotHandled;
+  const bool rot = ls[0].rot_scale != nullptr;
+  const int64_t d = ls[0].d, hb = rot ? ls[0].block : 1;
+  for (int i = 1; i < n_lin; ++i)
+    if (ls[i].d != d || (rot && ls[i].block != hb) || ls[i].x != ls[0].x || ls[i].ldx != ls[0].ldx)
+      return kLinearNotHandled;
+  if (rot && hb > 4096) return kLinearNotHandled;
+  Geom g0;
+  if (tiled_geom(ls[0].n, d, bits, &g0) != TP_OK) return kLinearNotHandled;
+  const int64_t G4 = g0.G4;
+  if (rot && hb > 2 * kChunkCols && G4 * kChunkCols != d) return kLinearNotHandled;
+  const bool big = rot && hb > 2 * kChunkCols;
+  int64_t T[kLinMaxParts];
+  for (int i = 0; i < n_lin; ++i) {
+    Geom g;
+    if (tiled_geom(ls[i].n, d, bits, &g) != TP_OK) return kLinearNotHandled;
+    T[i] = g.T;
+  }
+  const int cus = device_cu_count();
+  const bool ws_ok = ls[0].workspace && !((uintptr_t)ls[0].workspace & 15);
+  const LinPlan best = plan_linear(n_lin, T, G4, d, hb, rot, batch, bits, ws_ok,
+                                   ws_ok ? ls[0].workspace_bytes : 0, cus, (int64_t)device_max_lds());
   if (best.kparts == 0) return kLinearNotHandled;
 
   const int64_t zstride = best.pu * kChunkCols + 8;
@@ -791,3 +803,38 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
 }
 
 }  // namespace tp
+
+using namespace tp;
+
+extern "C" int tp_linear_forward_plan(const int64_t* ns, int n_linears, int64_t d, int64_t block, int bits,
+                                      int64_t batch, int64_t workspace_bytes, int cus, int64_t lds_bytes,
+                                      int64_t* out) {
+  if (!ns || !out) return TP_ERR_NULL_POINTER;
+  for (int i = 0; i < 6; ++i) out[i] = 0;
+  if (n_linears < 1 || n_linears > kLinMaxParts || cus < 1 || lds_bytes < 1 || d < 1) return TP_ERR_BAD_DIMS;
+  if (bits < 2 || bits > 4) return TP_ERR_UNSUPPORTED_BITS;
+  if (block < 1 || (block & (block - 1)) || d % block) return TP_ERR_BAD_BLOCK;
+  if (batch < 1 || batch > 8 || block > 4096) return TP_OK;  // not the one-pass kernel's
+  Geom g0;
+  int st = tiled_geom(ns[0], d, bits, &g0);
+  if (st) return st;
+  if (block > 2 * kChunkCols && g0.G4 * kChunkCols != d) return TP_OK;
+  int64_t T[kLinMaxParts];
+  for (int i = 0; i < n_linears; ++i) {
+    Geom g;
+    st = tiled_geom(ns[i], d, bits, &g);
+    if (st) return st;
+    T[i] = g.T;
+  }
+  const LinPlan p = plan_linear(n_linears, T, g0.G4, d, block, true, batch, bits, workspace_bytes > 0,
+                                workspace_bytes, cus, lds_bytes);
+  if (p.kparts == 0) return TP_OK;
+  out[0] = p.kparts;
+  out[1] = p.pu;
+  out[2] = p.c;
+  out[3] = p.sc;
+  out[4] = p.tpw;
+  out[5] = p.groups * p.kparts;
+  return TP_OK;
+}
+
