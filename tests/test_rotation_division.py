@@ -1,7 +1,10 @@
-"""The stack rotation divides by sqrt(block) with a corrected reciprocal
-product instead of an IEEE division (div_by_block_root in
-turbopress_amd/csrc/tp_tiled_common.h; the stack rotation and the rotations
-inside the per-linear launches).  Restated here in C (fmaf) and checked against IEEE
+"""The rotations divide by sqrt(block) with a corrected reciprocal product
+instead of an IEEE division (turbopress_amd/csrc/tp_tiled_common.h:
+div_by_block_root, whose special cases -- signed zeros, infinities -- are a
+class test and a select, in the rotations inside the per-linear launches;
+div_by_block_root_fx, which settles them with v_div_fixup_f32, in the stack
+rotation).  Both restated here in C (fmaf, and the fix-up's cases as the
+ISA describes them) and checked against IEEE
 division for every Hadamard block 2..16384 on a strided sample of all fp32
 bit patterns plus the special values: the quotients are equal wherever
 |v / c| >= 2^-100; below that the residual underflows, and both quotients
@@ -21,12 +24,20 @@ C_SRC = r"""
 #include <string.h>
 static float f_of(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 static uint32_t u_of(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
-/* div_by_block_root: q = v r, e = fma(-q, c, v), q1 = fma(e, r, q); q itself for q = +-0, +-inf */
+/* div_by_block_root: q = v r, e = fma(-q, c, v), q1 = fma(e, r, q); q itself for q = +-0, +-inf.
+   div_by_block_root_fx: the same q1, then v_div_fixup_f32(q1, c, v), which for a finite c > 0 whose
+   exponent keeps its underflow clause out of reach returns: a quiet NaN for a NaN v, the signed
+   infinity for v = +-inf, the signed zero for v = +-0, else |q1| with the sign of v. */
+static int variant;
 static float kernel_div(float v, float c, float r) {
   const float q = v * r;
   const float e = fmaf(-q, c, v);
   const float q1 = fmaf(e, r, q);
-  return (q == 0.0f || isinf(q)) ? q : q1;
+  if (variant == 0) return (q == 0.0f || isinf(q)) ? q : q1;
+  if (isnan(v)) return v;
+  if (isinf(v)) return copysignf(INFINITY, v);
+  if (v == 0.0f) return copysignf(0.0f, v);
+  return copysignf(fabsf(q1), v);
 }
 static int check(float v, float c, float r, unsigned long long* bad) {
   if (isnan(v)) return 0;
@@ -43,11 +54,13 @@ int main(int argc, char** argv) {
   unsigned long long bad = 0, n = 0;
   const uint32_t special[] = {0x00000000u, 0x80000000u, 0x7f800000u, 0xff800000u, 0x00000001u, 0x80000001u,
                               0x007fffffu, 0x00800000u, 0x7f7fffffu, 0xff7fffffu, 0x3f800000u, 0xbf800000u};
-  for (int j = 1; j <= 14; ++j) {
-    const float c = sqrtf((float)(1 << j));
-    const float r = 1.0f / c;
-    for (uint64_t u = 0; u < (1ull << 32); u += stride) { check(f_of((uint32_t)u), c, r, &bad); ++n; }
-    for (unsigned s = 0; s < sizeof(special) / sizeof(special[0]); ++s) { check(f_of(special[s]), c, r, &bad); ++n; }
+  for (variant = 0; variant < 2; ++variant) {
+    for (int j = 1; j <= 14; ++j) {
+      const float c = sqrtf((float)(1 << j));
+      const float r = 1.0f / c;
+      for (uint64_t u = 0; u < (1ull << 32); u += stride) { check(f_of((uint32_t)u), c, r, &bad); ++n; }
+      for (unsigned s = 0; s < sizeof(special) / sizeof(special[0]); ++s) { check(f_of(special[s]), c, r, &bad); ++n; }
+    }
   }
   printf("%llu %llu\n", n, bad);
   return bad != 0;

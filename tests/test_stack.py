@@ -221,12 +221,15 @@ def test_batch32_stack_mixed_blocks(cuda):
         assert O.max_rel(stack.outputs[i].float().cpu().numpy(), ref) <= GEMV_TOL, shapes[i]
 
 
-@pytest.mark.parametrize("batch", [3, 9])
+@pytest.mark.parametrize("batch", [1, 3, 9, 32])
 def test_stack_rotation_bit_exact(cuda, batch):
     """The rotation launch's z rows (the plan's last region, one [batch,
     G4 * 256] fp16 block per linear in order) equal the oracle's
     fp16(blockFWHT(x * rot_scale)) bit for bit, zero past d, for Hadamard
-    blocks 4..16384; batch 9 runs tile items of 4, 4 and 1 rows."""
+    blocks 4..16384.  Blocks of at most 4096 columns are packed across batch
+    rows into 4096-column tiles (d = 12, block 4: one tile holds every row;
+    d = 2560 at batch 3: a tile of 8 blocks spans rows 0 and 1, the last
+    tile is partial); larger blocks run per row."""
     from turbopress_amd.decode_step import LinearStack
     from turbopress_amd.runtime import PackedTCQLinear
     ds = [12, 40, 96, 128, 576, 1024, 2048, 2560, 3072, 4096, 6144, 8192, 9728, 16384]
@@ -251,6 +254,51 @@ def test_stack_rotation_bit_exact(cuda, batch):
         ref = O.rotate_activations(payload_numpy(p), x.cpu().numpy()).astype(np.float16).view(np.uint16)
         assert np.array_equal(got[:, :d], ref), (d, int(p["block"]))
         assert not got[:, d:].any(), d
+
+
+@pytest.mark.parametrize("batch", [3, 5])
+def test_stack_rotation_special_values(cuda, batch):
+    """Zeros of both signs and infinities through the rotation launch (16 and
+    64 columns per thread at batch 3 and 5; blocks 4, 512, 4096 and 8192):
+    a row of +0, a row of -0 (products with the negative signs are -0, and
+    every zero z carries the sign IEEE arithmetic gives it, which the
+    division's fix-up keeps), a row of random values with -0 entries and
+    one +inf per Hadamard block (an infinite z everywhere in that block).  z
+    equals the oracle's bit for bit wherever the oracle's is not NaN, and is
+    NaN where it is."""
+    from turbopress_amd.decode_step import LinearStack
+    from turbopress_amd.runtime import PackedTCQLinear
+    ds = [12, 2560, 4096, 8192]
+    payloads, entries = [], []
+    for i, d in enumerate(ds):
+        p = make_payload(16, d, 3, 64, seed=700 + i)
+        payloads.append(p)
+        gen = torch.Generator().manual_seed(800 + i)
+        x = (torch.randn(batch, d, generator=gen) * 3).to(torch.float16)
+        x[0] = 0.0
+        x[1] = -0.0
+        x[2, 5::13] = -0.0
+        x[2, ::int(p["block"])] = float("inf")
+        entries.append((PackedTCQLinear(p, mode="hip"), x.to(cuda), 0))
+    stack = LinearStack(entries)
+    stack.rotate()
+    torch.cuda.synchronize()
+    widths = [-(-d // 256) * 256 for d in ds]
+    zbytes = [batch * w * 2 for w in widths]
+    plan = stack.plan.cpu().numpy()
+    off = plan.size - sum(zbytes)
+    for p, (_, x, _), w, nb in zip(payloads, entries, widths, zbytes):
+        got = plan[off:off + nb].view(np.uint16).reshape(batch, w)
+        off += nb
+        d = int(p["d"])
+        with np.errstate(invalid="ignore"):
+            ref = O.rotate_activations(payload_numpy(p), x.cpu().numpy()).astype(np.float16)
+        g16 = got[:, :d].view(np.float16)
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(g16), nan), d
+        assert np.array_equal(got[:, :d][~nan], ref.view(np.uint16)[~nan]), d
+        # (the cases occur: zeros of both signs, infinities)
+        assert np.signbit(ref[:2]).any() and (~np.signbit(ref[:2])).any() and np.isinf(ref[2]).all(), d
 
 
 @pytest.mark.parametrize("shapes", ["qwen3-0.6b", "qwen3-4b"])

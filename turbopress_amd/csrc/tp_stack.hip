@@ -82,27 +82,30 @@ struct StackInfo {
   int32_t total_blocks;
   int32_t n_phases;
   int32_t batch;
-  int32_t n_rot;          // rotation tiles (batch * 4096-column tiles per linear) when the plan has a z buffer
+  int32_t n_rot;          // rotation tiles (see rot_tiles) when the plan has a z buffer
   int32_t min_g4;         // shortest K of the plan in 256-column units
   int64_t zbuf_bytes;
   int32_t total_wide;     // wide blocks (16 tiles x full K) of the batch 5..32 kernel
   int32_t total_k;        // blocks of the ordered kernel (tile groups with K split across the waves)
+  int32_t n_rot_packed;   // the first n_rot rotation tiles: packed tiles (blocks <= 4096); the rest above 4096
 };
 
-// One rotation tile (4096 columns of one batch row of one linear's input),
-// self-contained so that the rotation kernel starts from a single scalar
-// load: input row, rot_scale and z row bases, tile index and the linear's
-// sizes.
+// One rotation item: a 4096-column tile, as a packed tile or one batch row's
+// tile of a block above 4096 (see the rotation kernels).
 struct RotItem {
-  const uint16_t* x;    // input row (x + b * ldx)
+  const uint16_t* x;    // input row 0 (packed) / the tile's input row
   const uint16_t* rs;   // rot_scale [d]
-  uint16_t* z;          // z row in the plan's z buffer
-  int32_t k;            // tile index along d
+  uint16_t* z;          // z row 0 (packed) / the tile's z row
+  int32_t k;            // packed: first block of the tile (row-major over batch rows); else tile index along d
   int32_t d;
-  int32_t hb;           // Hadamard block
-  int32_t zld;          // z columns written (G4 * 256; zero past d)
+  int32_t hb;
+  int32_t zld;          // z columns per batch row
   float hdiv;           // fp32(sqrt(hb))
-  int32_t reserved[5];
+  int32_t ldx;          // packed: input row stride (elements)
+  int32_t nblk;         // packed: blocks per batch row (d / hb)
+  int32_t nbt;          // packed: blocks of the linear (batch * nblk)
+  int32_t logh;         // log2(hb)
+  float hrecip;         // fp32(1 / hdiv), correctly rounded
 };
 static_assert(sizeof(RotItem) == 64, "one 16-dword scalar load per rotation tile");
 
@@ -232,112 +235,163 @@ __device__ inline void wait_phase(const StackRO& P, uint32_t* pdone, StackCounte
 // ---------------------------------------------------------------------------
 // 1. rotation of every linear's input into the plan's z buffer
 // ---------------------------------------------------------------------------
-// One workgroup of 256 threads transforms a tile of up to 4096 columns of
-// one batch row (tiles start at multiples of 4096, so a Hadamard block of at
-// most 4096 never straddles two tiles).  Thread t holds columns 16t..16t+15:
-// butterflies at distance 1..8 run in registers, 16..512 across lanes,
-// 1024 and 2048 as one radix-4 step through LDS -- the stage order of the
-// reference's transform (distance 1, 2, 4, ... then one division by
-// sqrt(block)), all in fp32, z rounded to fp16 once.  A block larger than
-// 4096 (H_hb = H_(hb/4096) (x) H_4096) transforms each of its 4096-column
-// sub-tiles, then runs the stages across sub-tiles (4096, 8192) in order.
+// z = blockFWHT(x * rot_scale) / sqrt(hb) in fp32, rounded to fp16 once,
+// with the stage order of the reference's transform (distance 1, 2, 4, ...
+// then one division by sqrt(block)).
+//
+// Blocks of at most 4096 columns: a linear's (batch row, block) pairs,
+// row-major, are packed densely into tiles of 4096 columns (4096 / hb
+// blocks per tile, from as many batch rows as that takes), one 256-thread
+// workgroup per tile, so that no work goes to columns past d (a
+// 2560-column input at batch 32 is 20 tiles, not 32 tiles of 4096).
+//
+// Thread (wave w, lane l) holds tile columns 1024 w + 256 g + 4 m(l) + j,
+// g, j = 0..3: every 8-byte load or store of the wave covers 512
+// contiguous bytes.  (Threads holding 16 contiguous columns measured the
+// same; 32 or 64 contiguous columns per thread, fewer lane stages but 32 or
+// 64 cache lines per load, took 37.6 / 48.3 us at batch 32 against 24.)
+// At 16 columns per thread the launch is bound by its VALU issue.  Butterflies at
+// distance 1, 2 (j) and 256, 512 (g) run in registers, 4 .. 128 across
+// lanes (bits of m), 1024 and 2048 as one radix-4 step through LDS (the
+// wave).  m(l) puts lanes so that the partner of m bits 0..3 is one DPP
+// move: lane xor 1 / 2 / 7 / 8 (two quad permutes, the half-row mirror, a
+// row rotation by 8); bits 4 and 5 are lane xor 16 and 32 (bpermute).  The
+// stages are unrolled per block size (one instantiation per log2 hb), so
+// that no stage is skipped at run time.
+//
+// Blocks above 4096 (H_hb = H_(hb/4096) (x) H_4096): one workgroup per
+// 4096-column output tile of one batch row transforms each 4096-column
+// sub-tile of its block, then runs the stages across sub-tiles (4096, 8192)
+// in order.
 
 constexpr int kRotTile = 4096;
 constexpr int kRotThreads = 256;
-constexpr int kRotEPT = kRotTile / kRotThreads;  // 16
+constexpr int kRotEPT = kRotTile / kRotThreads;  // 16 columns per thread
+constexpr int kRotMaxLogH = 12;                  // packed tiles: blocks of 1 .. 4096
 
-__host__ __device__ inline int rot_tiles(int G4) { return (G4 * kChunkCols + kRotTile - 1) / kRotTile; }
+// Rotation tiles of one linear: packed tiles of its batch * d columns when
+// its block is at most 4096, else 4096-column tiles of each batch row.
+__host__ __device__ inline int64_t rot_tiles(int64_t batch, int64_t d, int64_t hb) {
+  return hb <= kRotTile ? (batch * d + kRotTile - 1) / kRotTile : batch * (d / kRotTile);
+}
 
+// m(l): lane bits 0 and 1 xor lane bit 2 (so that m bit 2 is lane xor 7),
+// every other bit as is.  The map is its own inverse.
+__device__ __forceinline__ int rot_lane_index(int lane) { return lane ^ (((lane >> 2) & 1) * 3); }
 
-// 16 halves at byte offset `off` of a buffer, as fp32.  The four 8-byte
-// loads are issued together; groups past the buffer's end read as zeros
-// (every d is a multiple of 4, so a group is wholly inside or outside).
-// Each load gets its own opaque offset register so that the compiler does
-// not merge two of them into one 16-byte access, which could straddle the
-// end of the buffer.
-__device__ __forceinline__ void load16(__amdgpu_buffer_rsrc_t r, uint32_t off, float v[kRotEPT]) {
-  u32x2_t w[kRotEPT / 4];
+// Tile column of element e (= 4 g + j) of thread (w, m).
+__device__ __forceinline__ int rot_col(int w, int m, int e) { return 1024 * w + 256 * (e >> 2) + 4 * m + (e & 3); }
+
+// The value of the lane whose m differs in bit K (K = 0..5); `lane4` is
+// the lane index times 4 (the byte address of a bpermute).
+template <int K>
+__device__ __forceinline__ float rot_partner(float v, int lane4) {
+  const int x = __builtin_bit_cast(int, v);
+  int y;
+  if constexpr (K == 0) y = __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false);        // quad_perm [1,0,3,2]
+  else if constexpr (K == 1) y = __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  else if constexpr (K == 2) y = __builtin_amdgcn_mov_dpp(x, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  else if constexpr (K == 3) y = __builtin_amdgcn_mov_dpp(x, 0x128, 0xF, 0xF, false);  // row_ror:8
+  else y = __builtin_amdgcn_ds_bpermute(lane4 ^ (4 << K), x);                         // lane xor 16 / 32
+  return __builtin_bit_cast(float, y);
+}
+
+// Butterflies at distance 4 << K across lanes, when that is below the
+// block: the lane whose m has bit K set keeps partner - own, the other
+// own + partner, each one FMA fma(+-1, own, partner) (the product is exact,
+// so the sum rounds as the add or subtract does).
+template <int K, int LOGH>
+__device__ __forceinline__ void rot_lane_stage(float v[kRotEPT], int m, int lane4) {
+  if constexpr ((4 << K) < (1 << LOGH)) {
+    // +-1.0: the sign bit from bit K of m
+    const float sg = __builtin_bit_cast(float, 0x3F800000u | (((uint32_t)m << (31 - K)) & 0x80000000u));
 #pragma unroll
-  for (int g = 0; g < kRotEPT / 4; ++g) {
-    uint32_t o = off + 8u * g;
-    __asm__("" : "+v"(o));
-    w[g] = __builtin_amdgcn_raw_buffer_load_b64(r, o, 0, 0);
-  }
-#pragma unroll
-  for (int g = 0; g < kRotEPT / 4; ++g) {
-    float t[4];
-    unpack4h(make_uint2(w[g][0], w[g][1]), t);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[4 * g + e] = t[e];
+    for (int e = 0; e < kRotEPT; ++e) v[e] = __builtin_fmaf(sg, v[e], rot_partner<K>(v[e], lane4));
   }
 }
 
-// v = x * rot_scale of 4096-column tile `k` of the item's row.
-__device__ __forceinline__ void rot_input(const TP_CONST RotItem& L, int k, int tid, float v[kRotEPT]) {
-  const uint32_t off = (uint32_t)(k * kRotTile + tid * kRotEPT) * 2u;
-  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(L.x, (uint32_t)L.d * 2u);
-  const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(L.rs, (uint32_t)L.d * 2u);
-  float rv[kRotEPT];
-  load16(xrs, off, v);
-  load16(rrs, off, rv);
+// Butterflies between elements e and e + S (element stride S = 2: column
+// distance 2; S = 4, 8: column distance 256, 512) when that distance is
+// below the block.
+template <int S, int DIST, int LOGH>
+__device__ __forceinline__ void rot_reg_stage(float v[kRotEPT]) {
+  if constexpr (DIST < (1 << LOGH)) {
 #pragma unroll
-  for (int e = 0; e < kRotEPT; ++e) v[e] *= rv[e];
+    for (int e = 0; e < kRotEPT; ++e) {
+      if ((e & S) == 0) {
+        const float a = v[e], c = v[e + S];
+        v[e] = a + c;
+        v[e + S] = a - c;
+      }
+    }
+  }
 }
 
-// Butterflies of a 4096-column tile at distances 1 .. hmax / 2 (hmax =
-// min(hb, 4096)), unnormalized.  `ex`: 4096 floats of LDS.  A butterfly's
-// two outputs a + b and a - b are one FMA each, fma(+-1, a, b): the product
-// is exact, so the sum rounds as the add or subtract does.
-__device__ __forceinline__ void rot_butterflies(float v[kRotEPT], int hmax, int tid, float* ex) {
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  // Stages are skipped with a (uniform) condition, never a loop exit: the
-  // loops must unroll so that every v[] index is a compile-time constant (a
-  // runtime stage distance would index the register array dynamically).
+__device__ __forceinline__ float hlo(uint32_t w) { return (float)__builtin_bit_cast(_Float16, (uint16_t)w); }
+__device__ __forceinline__ float hhi(uint32_t w) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)(w >> 16));
+}
+
+// v = x * rot_scale of the thread's 16 columns (4 groups of 4 halves, as
+// loaded) with the distance-1 butterflies when the block has them: the
+// product of two fp16 values is exact in fp32, so fma(x0, r0, +-x1 r1)
+// rounds as the add / subtract of the two products does.
+template <bool STAGE1>
+__device__ __forceinline__ void rot_products(const u32x2_t* xw, const u32x2_t* rw, float v[kRotEPT]) {
+  // x1 r1 as fma(x1, r1, -0) (exact; a -0 product keeps its sign), the -0 in
+  // an opaque register: a literal one lets the compiler turn the fma into a
+  // product of two converted halves (three instructions, not one)
+  float nz = -0.f;
+  __asm__("" : "+v"(nz));
 #pragma unroll
-  for (int h = 1; h < kRotEPT; h <<= 1) {
-    if (h < hmax) {
+  for (int g = 0; g < 4; ++g) {
 #pragma unroll
-      for (int e = 0; e < kRotEPT; ++e) {
-        if ((e & h) == 0) {
-          const float a = v[e], c = v[e + h];
-          v[e] = a + c;
-          v[e + h] = a - c;
-        }
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t xv = xw[g][w], rv = rw[g][w];
+      float* o = v + 4 * g + 2 * w;
+      const float b = __builtin_fmaf(hhi(xv), hhi(rv), nz);
+      if (STAGE1) {
+        o[0] = __builtin_fmaf(hlo(xv), hlo(rv), b);
+        o[1] = __builtin_fmaf(hlo(xv), hlo(rv), -b);
+      } else {
+        o[0] = __builtin_fmaf(hlo(xv), hlo(rv), nz);
+        o[1] = b;
       }
     }
   }
-  // distances 16..512: lane bit sft; the upper lane of a pair keeps p - v
+}
+
+// Every stage of a block of 2^LOGH columns (at most 4096) from distance 2
+// (rot_products ran the first), unnormalized.  `ex`: 4096 floats of LDS
+// (blocks of 2048 and 4096).
+template <int LOGH>
+__device__ __forceinline__ void rot_stages(float v[kRotEPT], int w, int m, int lane4, float* ex) {
+  constexpr int HB = 1 << LOGH;
+  rot_reg_stage<2, 2, LOGH>(v);
+  rot_lane_stage<0, LOGH>(v, m, lane4);
+  rot_lane_stage<1, LOGH>(v, m, lane4);
+  rot_lane_stage<2, LOGH>(v, m, lane4);
+  rot_lane_stage<3, LOGH>(v, m, lane4);
+  rot_lane_stage<4, LOGH>(v, m, lane4);
+  rot_lane_stage<5, LOGH>(v, m, lane4);
+  rot_reg_stage<4, 256, LOGH>(v);
+  rot_reg_stage<8, 512, LOGH>(v);
+  if constexpr (HB > 1024) {  // distances 1024 (and 2048): the wave
+    __syncthreads();  // the previous sub-tile's reads of ex are done
 #pragma unroll
-  for (int sft = 0; sft < 6; ++sft) {
-    if ((kRotEPT << sft) < hmax) {
-      const float sg = ((lane >> sft) & 1) ? -1.f : 1.f;
-#pragma unroll
-      for (int e = 0; e < kRotEPT; ++e) {
-        const float p = sft < 4 ? lane_xor_row(v[e], 1 << sft) : __shfl_xor(v[e], 1 << sft, 64);
-        v[e] = __builtin_fmaf(sg, v[e], p);
-      }
-    }
-  }
-  if (hmax > 1024) {  // distances 1024 (and 2048): wave bits of the column
-    __syncthreads();  // the previous item's reads of ex are done
-#pragma unroll
-    for (int e = 0; e < kRotEPT; ++e) ex[tid * kRotEPT + e] = v[e];
+    for (int e = 0; e < kRotEPT; ++e) ex[rot_col(w, m, e)] = v[e];
     __syncthreads();
-    const int i0 = (lane * kRotEPT) & 1023;
-    const float s1 = (wave & 1) ? -1.f : 1.f;
-    if (hmax == 2048) {
+    const float s1 = (w & 1) ? -1.f : 1.f;
+    if constexpr (HB == 2048) {
 #pragma unroll
-      for (int e = 0; e < kRotEPT; ++e) {
-        const float p = ex[(wave ^ 1) * 1024 + i0 + e];
-        v[e] = __builtin_fmaf(s1, v[e], p);
-      }
+      for (int e = 0; e < kRotEPT; ++e) v[e] = __builtin_fmaf(s1, v[e], ex[rot_col(w ^ 1, m, e)]);
     } else {
-      const float s2 = (wave & 2) ? -1.f : 1.f;
+      const float s2 = (w & 2) ? -1.f : 1.f;
 #pragma unroll
       for (int e = 0; e < kRotEPT; ++e) {
-        const float u0 = ex[i0 + e], u1 = ex[1024 + i0 + e], u2 = ex[2048 + i0 + e], u3 = ex[3072 + i0 + e];
-        // natural-order H_4 row `wave`: stage 1024 then stage 2048
+        const int i0 = rot_col(0, m, e);
+        const float u0 = ex[i0], u1 = ex[1024 + i0], u2 = ex[2048 + i0], u3 = ex[3072 + i0];
+        // natural-order H_4 row w: stage 1024 then stage 2048
         const float s01 = __builtin_fmaf(s1, u1, u0);
         const float s23 = __builtin_fmaf(s1, u3, u2);
         v[e] = __builtin_fmaf(s2, s23, s01);
@@ -346,80 +400,188 @@ __device__ __forceinline__ void rot_butterflies(float v[kRotEPT], int hmax, int 
   }
 }
 
-// z = v / sqrt(hb) in fp16 into the item's z row (zero past d).
-__device__ __forceinline__ void rot_store(const TP_CONST RotItem& L, const float v[kRotEPT], int tid) {
-  const int c0 = L.k * kRotTile + tid * kRotEPT;
-  const int zld = L.zld;  // columns written (zero past d)
-  uint16_t* zr = L.z;
-  const float c = L.hdiv, r = 1.f / c;
+// z of 4 columns of a block of 2^LOGH columns, v / sqrt(hb) correctly
+// rounded (for even LOGH sqrt(hb) is a power of two and the product with
+// its reciprocal is the quotient), as 4 halves.
+template <int LOGH>
+__device__ __forceinline__ u32x2_t rot_z4(const float* v, float c, float r) {
+  float q[4];
 #pragma unroll
-  for (int g = 0; g < kRotEPT / 4; ++g) {
-    if (c0 + 4 * g >= zld) break;
-    float z4[4];
+  for (int e = 0; e < 4; ++e) q[e] = (LOGH & 1) ? div_by_block_root_fx(v[e], c, r) : v[e] * r;
+  return u32x2_t{pack_h2(q[0], q[1]), pack_h2(q[2], q[3])};
+}
+
+// Four halves at element offset `o` of a buffer (out of range: zeros).
+// Each load keeps its own opaque offset register so that the compiler does
+// not merge two into one 16-byte access, which could straddle the end of
+// the buffer (every d is a multiple of 4, so a group is wholly inside or
+// outside).
+__device__ __forceinline__ u32x2_t load4h(__amdgpu_buffer_rsrc_t r, uint32_t o) {
+  uint32_t b = o * 2u;
+  __asm__("" : "+v"(b));
+  return __builtin_amdgcn_raw_buffer_load_b64(r, b, 0, 0);
+}
+
+// One packed tile: load x * rot_scale, transform, divide, store z.
+template <int LOGH>
+__device__ __forceinline__ void rot_packed_tile(const TP_CONST RotItem& L, int w, int m, int lane4, float* ex) {
+  constexpr int HB = 1 << LOGH;
+  const uint32_t nblk = (uint32_t)L.nblk, nbt = (uint32_t)L.nbt, ldx = (uint32_t)L.ldx;
+  const uint32_t batch = nbt / nblk;
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(L.x, (uint32_t)((int64_t)(batch - 1) * ldx + L.d) * 2u);
+  const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(L.rs, (uint32_t)L.d * 2u);
+  // group g: tile columns 1024 w + 256 g + 4 m .. + 3, in block gb, batch
+  // row b, columns col .. col + 3 of that row
+  bool ok[4];
+  uint32_t b[4], col[4];
+  u32x2_t xw[4], rw[4];
+  if constexpr (HB >= 256) {
+    // the block and row are the wave's (scalar), the column inside the
+    // block the lane's: one add per load.  A group past the tile's blocks
+    // (the last tile) loads from byte offset 2^31 + 8 m (out of range:
+    // zeros) and stores nothing.
+    const uint32_t m8 = 8u * (uint32_t)m;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) z4[e] = div_by_block_root(v[4 * g + e], c, r);
-    const u32x2_t w = {(uint32_t)f2h(z4[0]) | ((uint32_t)f2h(z4[1]) << 16),
-                       (uint32_t)f2h(z4[2]) | ((uint32_t)f2h(z4[3]) << 16)};
-    *(TP_GLOBAL u32x2_t*)(zr + c0 + 4 * g) = w;
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t base = 1024u * (uint32_t)w + 256u * g;
+      const uint32_t blk = (uint32_t)L.k + (base >> LOGH);
+      const uint32_t row = (uint32_t)__builtin_amdgcn_readfirstlane((int)(blk / nblk));
+      ok[g] = blk < nbt;
+      b[g] = row;
+      const uint32_t cu = (blk - row * nblk) * HB + (base & (HB - 1));  // (uniform)
+      col[g] = cu + 4u * (uint32_t)m;
+      const uint32_t xb = ok[g] ? (row * ldx + cu) * 2u : 0x80000000u;
+      const uint32_t rb = ok[g] ? cu * 2u : 0x80000000u;
+      uint32_t xo = xb + m8, ro = rb + m8;
+      __asm__("" : "+v"(xo), "+v"(ro));
+      xw[g] = __builtin_amdgcn_raw_buffer_load_b64(xrs, xo, 0, 0);
+      rw[g] = __builtin_amdgcn_raw_buffer_load_b64(rrs, ro, 0, 0);
+    }
+  } else {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t q = 1024u * (uint32_t)w + 256u * g + 4u * (uint32_t)m;
+      const uint32_t gb = (uint32_t)L.k + (q >> LOGH);
+      ok[g] = gb < nbt;
+      b[g] = gb / nblk;
+      col[g] = (gb - b[g] * nblk) * HB + (q & (HB - 1));
+      xw[g] = load4h(xrs, ok[g] ? b[g] * ldx + col[g] : kOutOfRange / 2u);
+      rw[g] = load4h(rrs, ok[g] ? col[g] : kOutOfRange / 2u);
+    }
+  }
+  float v[kRotEPT];
+  rot_products<(LOGH > 0)>(xw, rw, v);
+  rot_stages<LOGH>(v, w, m, lane4, ex);
+  const float c = L.hdiv, r = L.hrecip;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    if (!ok[g]) continue;
+    *(TP_GLOBAL u32x2_t*)(L.z + (size_t)b[g] * L.zld + col[g]) = rot_z4<LOGH>(v + 4 * g, c, r);
   }
 }
 
-// One workgroup per tile when the host knows the tile count (ONE_TILE: the
-// descriptor is the first load, the x / rot_scale loads the second);
-// otherwise a grid-stride loop bounded by the plan's count.  BIG selects the
-// tiles of blocks above 4096 columns (their registers would halve the
-// occupancy of the common case), !BIG the others; a plan with big blocks
-// gets both launches.
-template <bool ONE_TILE, bool BIG>
+// Packed tiles (items [0, n_rot_packed) of the plan), one workgroup per
+// tile when the host knows the tile count (ONE_TILE: the descriptor is the
+// first load, the x / rot_scale loads the second); otherwise a grid-stride
+// loop bounded by the plan's count.
+template <bool ONE_TILE>
 __global__ void __launch_bounds__(kRotThreads)
 tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
   __shared__ float ex[kRotTile];
   const int first = blockIdx.x;
-  const int end = ONE_TILE ? first + 1 : cread(reinterpret_cast<const StackInfo*>(plan_ro)).n_rot;
+  const int end = ONE_TILE ? first + 1 : cread(reinterpret_cast<const StackInfo*>(plan_ro)).n_rot_packed;
   const int step = ONE_TILE ? 1 : (int)gridDim.x;
   const RotItem* items = reinterpret_cast<const RotItem*>(plan_ro + (kRotItems - kStackRO));
-  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = (int)threadIdx.x & 63;
+  const int m = rot_lane_index(lane), lane4 = 4 * lane;
   for (int item = first; item < end; item += step) {
     const TP_CONST RotItem& L = cread(items + item);
-    // the descriptor's fields in one round trip (the size test below, left
-    // alone, had hb loaded first and the rest after its wait)
-    __asm__ volatile("" ::"s"(L.x), "s"(L.rs), "s"(L.k), "s"(L.d), "s"(L.hb) : "memory");
-    if ((L.hb > kRotTile) != BIG) continue;  // (uniform)
-    float v[kRotEPT];
-    if (!BIG) {
-      rot_input(L, L.k, tid, v);
-      rot_butterflies(v, L.hb, tid, ex);
-    } else {
-      // H_hb = H_(hb/4096) (x) H_4096, stages in order of distance: every
-      // 4096-column sub-tile of the block through distances 1..2048, then
-      // distance 4096 (sub-tile pairs) and 8192 (pairs of pairs); sub-tile o
-      // of the result takes the signs of row o.
-      const int nsub = L.hb / kRotTile;        // 2 or 4
-      const int o = L.k % nsub, k0 = L.k - o;  // this tile's sub-tile, the block's first
-      const float s1 = (o & 1) ? -1.f : 1.f, s2 = (o & 2) ? -1.f : 1.f;
-      float a[kRotEPT];
+    // the descriptor's fields in one round trip
+    __asm__ volatile("" ::"s"(L.x), "s"(L.rs), "s"(L.z), "s"(L.k), "s"(L.d), "s"(L.zld), "s"(L.hdiv),
+                     "s"(L.ldx), "s"(L.nblk), "s"(L.nbt), "s"(L.logh), "s"(L.hrecip)
+                     : "memory");
+    switch (L.logh) {  // (uniform)
+      case 0: rot_packed_tile<0>(L, w, m, lane4, ex); break;
+      case 1: rot_packed_tile<1>(L, w, m, lane4, ex); break;
+      case 2: rot_packed_tile<2>(L, w, m, lane4, ex); break;
+      case 3: rot_packed_tile<3>(L, w, m, lane4, ex); break;
+      case 4: rot_packed_tile<4>(L, w, m, lane4, ex); break;
+      case 5: rot_packed_tile<5>(L, w, m, lane4, ex); break;
+      case 6: rot_packed_tile<6>(L, w, m, lane4, ex); break;
+      case 7: rot_packed_tile<7>(L, w, m, lane4, ex); break;
+      case 8: rot_packed_tile<8>(L, w, m, lane4, ex); break;
+      case 9: rot_packed_tile<9>(L, w, m, lane4, ex); break;
+      case 10: rot_packed_tile<10>(L, w, m, lane4, ex); break;
+      case 11: rot_packed_tile<11>(L, w, m, lane4, ex); break;
+      case 12: rot_packed_tile<12>(L, w, m, lane4, ex); break;
+      default: break;
+    }
+  }
+}
+
+// Tiles of blocks above 4096 (items [n_rot_packed, n_rot) of the plan).
+// H_hb = H_(hb/4096) (x) H_4096, stages in order of distance: every
+// 4096-column sub-tile of the block through distances 1..2048, then
+// distance 4096 (sub-tile pairs) and 8192 (pairs of pairs); sub-tile o of
+// the result takes the signs of row o.
+template <bool ONE_TILE>
+__global__ void __launch_bounds__(kRotThreads)
+tcq_stack_rotate_big_kernel(const char* __restrict__ plan_ro) {
+  __shared__ float ex[kRotTile];
+  const TP_CONST StackInfo& ci = cread(reinterpret_cast<const StackInfo*>(plan_ro));
+  const int base = ci.n_rot_packed;
+  const int first = base + (int)blockIdx.x;
+  const int end = ONE_TILE ? first + 1 : ci.n_rot;
+  const int step = ONE_TILE ? 1 : (int)gridDim.x;
+  const RotItem* items = reinterpret_cast<const RotItem*>(plan_ro + (kRotItems - kStackRO));
+  const int w = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int lane = (int)threadIdx.x & 63;
+  const int m = rot_lane_index(lane), lane4 = 4 * lane;
+  for (int item = first; item < end; item += step) {
+    const TP_CONST RotItem& L = cread(items + item);
+    __asm__ volatile("" ::"s"(L.x), "s"(L.rs), "s"(L.z), "s"(L.k), "s"(L.d), "s"(L.hb), "s"(L.zld), "s"(L.hdiv),
+                     "s"(L.hrecip)
+                     : "memory");
+    const int nsub = L.hb / kRotTile;        // 2 or 4
+    const int o = L.k % nsub, k0 = L.k - o;  // this tile's sub-tile, the block's first
+    const float s1 = (o & 1) ? -1.f : 1.f, s2 = (o & 2) ? -1.f : 1.f;
+    const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(L.x, (uint32_t)L.d * 2u);
+    const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(L.rs, (uint32_t)L.d * 2u);
+    float v[kRotEPT], a[kRotEPT];
 #pragma unroll 1
-      for (int i = 0; i < nsub; ++i) {
-        float t[kRotEPT];
-        rot_input(L, k0 + i, tid, t);
-        rot_butterflies(t, kRotTile, tid, ex);
-        if ((i & 1) == 0) {
+    for (int i = 0; i < nsub; ++i) {
+      u32x2_t xw[4], rw[4];
 #pragma unroll
-          for (int e = 0; e < kRotEPT; ++e) a[e] = t[e];
+      for (int g = 0; g < 4; ++g) {
+        const uint32_t off = (uint32_t)((k0 + i) * kRotTile + rot_col(w, m, 4 * g));
+        xw[g] = load4h(xrs, off);
+        rw[g] = load4h(rrs, off);
+      }
+      float t[kRotEPT];
+      rot_products<true>(xw, rw, t);
+      rot_stages<kRotMaxLogH>(t, w, m, lane4, ex);
+      if ((i & 1) == 0) {
+#pragma unroll
+        for (int e = 0; e < kRotEPT; ++e) a[e] = t[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < kRotEPT; ++e) a[e] = __builtin_fmaf(s1, t[e], a[e]);  // distance 4096
+        if (i == 1) {
+#pragma unroll
+          for (int e = 0; e < kRotEPT; ++e) v[e] = a[e];
         } else {
 #pragma unroll
-          for (int e = 0; e < kRotEPT; ++e) a[e] = __builtin_fmaf(s1, t[e], a[e]);  // distance 4096
-          if (i == 1) {
-#pragma unroll
-            for (int e = 0; e < kRotEPT; ++e) v[e] = a[e];
-          } else {
-#pragma unroll
-            for (int e = 0; e < kRotEPT; ++e) v[e] = __builtin_fmaf(s2, a[e], v[e]);  // distance 8192
-          }
+          for (int e = 0; e < kRotEPT; ++e) v[e] = __builtin_fmaf(s2, a[e], v[e]);  // distance 8192
         }
       }
     }
-    rot_store(L, v, tid);
+    // z = v / sqrt(hb) into the item's z row (hb > 4096 divides d: zld = d);
+    // log2 hb is 13 or 14: the corrected quotient serves both
+    const float c = L.hdiv, r = L.hrecip;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *(TP_GLOBAL u32x2_t*)(L.z + L.k * kRotTile + rot_col(w, m, 4 * g)) = rot_z4<1>(v + 4 * g, c, r);
   }
 }
 
@@ -1343,8 +1505,7 @@ __device__ __forceinline__ ZChunk wide_rotate(const XChunk& c, int lane, int hb,
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-      z.v[k][e] = (uint32_t)f2h(div_by_block_root(v[2 * e], hdiv, rdiv)) |
-                  ((uint32_t)f2h(div_by_block_root(v[2 * e + 1], hdiv, rdiv)) << 16);
+      z.v[k][e] = pack_h2(div_by_block_root(v[2 * e], hdiv, rdiv), div_by_block_root(v[2 * e + 1], hdiv, rdiv));
   }
   return z;
 }
@@ -1788,8 +1949,8 @@ int linear_forward_wide(const LinearDesc& Lin, const uint16_t* z, int64_t zld, i
 // rotation tile count, blocks, batch and layout offsets.  A plan the process
 // did not initialise gets kernels that read these from the plan header.
 struct PlanReg {
-  int n_rot, total, batch, total_k;
-  bool big_rot;  // some linear has a Hadamard block above 4096 columns
+  int n_rot_packed, n_rot_big;  // rotation tiles of blocks <= 4096 / above 4096
+  int total, batch, total_k;
   int64_t lin_off, sched_o_off, sched_u_off;
 };
 std::mutex g_plan_mutex;
@@ -1846,6 +2007,7 @@ int launch_gemv(char* plan, int64_t total_blocks, int64_t batch, const uint16_t*
 struct StackSizes {
   int n_phases;
   int64_t total_blocks, n_rot, zbuf_bytes, min_g4;
+  int64_t n_rot_packed;  // rotation tiles of blocks <= 4096 (the first n_rot_packed of n_rot)
 };
 
 inline int64_t zbuf_linear_bytes(int64_t batch, int64_t G4) { return (batch * G4 * kChunkCols * 2 + 255) & ~(int64_t)255; }
@@ -1853,7 +2015,7 @@ inline int64_t zbuf_linear_bytes(int64_t batch, int64_t G4) { return (batch * G4
 inline int stack_sizes(const tp_stack_linear* linears, int n_linears, int bits, int64_t batch, StackSizes* out) {
   if (!linears) return TP_ERR_NULL_POINTER;
   if (n_linears < 1 || n_linears > kStackMaxLinears || batch < 1 || batch > 32) return TP_ERR_BAD_DIMS;
-  StackSizes z = {1, 0, 0, 0, INT32_MAX};
+  StackSizes z = {1, 0, 0, 0, INT32_MAX, 0};
   for (int i = 0; i < n_linears; ++i) {
     const tp_stack_linear& l = linears[i];
     if (l.phase < 0 || l.phase >= kStackMaxPhases) return TP_ERR_BAD_DIMS;
@@ -1870,7 +2032,14 @@ inline int stack_sizes(const tp_stack_linear* linears, int n_linears, int bits, 
     if (blocks >= (1 << kStackBlockBits)) return TP_ERR_BAD_DIMS;
     z.total_blocks += blocks;
     if (g.G4 < z.min_g4) z.min_g4 = g.G4;
-    z.n_rot += batch * rot_tiles((int)g.G4);
+    // (a block that is no power of 2 dividing d is refused by the plan's
+    // set-up; it adds no rotation tiles here)
+    const int64_t hb = l.block;
+    if (hb >= 1 && !(hb & (hb - 1)) && l.d % hb == 0 && hb <= 16384) {
+      const int64_t tiles = rot_tiles(batch, l.d, hb);
+      z.n_rot += tiles;
+      if (hb <= kRotTile) z.n_rot_packed += tiles;
+    }
     z.zbuf_bytes += zbuf_linear_bytes(batch, g.G4);
   }
   // z buffer offsets are 32-bit and lanes past the batch read at 2^31: keep it below 2 GiB
@@ -1901,8 +2070,10 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
   const StackLayout lay = stack_layout(n_linears, z.n_phases, (int)z.total_blocks, (int)z.n_rot, z.zbuf_bytes);
   if (plan_bytes < (int64_t)lay.total) return TP_ERR_WORKSPACE;
   if ((uintptr_t)plan & 255) return TP_ERR_MISALIGNED;
-  // Everything before the z buffer is written from the host; every run
-  // fills the z buffer before reading it.
+  // Everything before the z buffer is written from the host; the z buffer
+  // is cleared once here (its columns past d stay zero: the rotation writes
+  // only the columns of whole blocks) and every run fills the rest before
+  // reading it.
   char* host = (char*)calloc(1, lay.zbuf);
   if (!host) return TP_ERR_HIP;
   StackInfo* h = reinterpret_cast<StackInfo*>(host + kStackRO);
@@ -1917,10 +2088,9 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
   int32_t* ptiles = reinterpret_cast<int32_t*>(host + lay.ptiles);
   OrdBlockDesc* oblk = reinterpret_cast<OrdBlockDesc*>(host + lay.oblk);
   int64_t total_k = 0;
-  bool big_rot = false;
   RotItem* items = reinterpret_cast<RotItem*>(host + lay.rot_items);
   char* zbuf = reinterpret_cast<char*>(plan) + lay.zbuf;
-  int64_t total = 0, rot = 0, zoff = 0;
+  int64_t total = 0, rot_p = 0, rot_b = 0, zoff = 0;
   for (int i = 0; i < n_linears; ++i) {
     const tp_stack_linear& l = linears[i];
     Geom g;
@@ -1931,7 +2101,6 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     }
     const int64_t hb = l.block;
     if (hb < 1 || (hb & (hb - 1)) || l.d % hb || hb > 16384) { st = TP_ERR_BAD_BLOCK; break; }
-    if (hb > kRotTile) big_rot = true;
     if (l.ldx < l.d || (l.ldx & 3) || (l.d & 3) || ((uintptr_t)l.x & 7) || ((uintptr_t)l.rot_scale & 7) ||
         ((uintptr_t)l.path_tiled & 15) || ((uintptr_t)l.member_tiled & 15)) {
       st = TP_ERR_MISALIGNED;
@@ -1967,19 +2136,45 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     ptiles[l.phase] += L.T;
     total += L.blocks;
     if (z.zbuf_bytes) {
-      const int ntiles = rot_tiles((int)g.G4);
       const int zld = (int)g.G4 * kChunkCols;
-      for (int64_t b = 0; b < batch; ++b) {
-        for (int k = 0; k < ntiles; ++k) {
-          RotItem& R = items[rot++];
-          R.x = l.x + b * l.ldx;
+      if (hb <= kRotTile) {
+        // packed tiles over the (batch row, block) pairs; every x load is
+        // range-checked against the span of the batch rows, which must stay
+        // below the 2^31-byte offset of the loads past the last block
+        if (((batch - 1) * l.ldx + l.d) * 2 > (int64_t)INT32_MAX) { st = TP_ERR_BAD_DIMS; break; }
+        const int64_t nblk = l.d / hb, bpt = kRotTile / hb;
+        const int64_t tiles = rot_tiles(batch, l.d, hb);
+        for (int64_t t = 0; t < tiles; ++t) {
+          RotItem& R = items[rot_p++];
+          R.x = l.x;
           R.rs = l.rot_scale;
-          R.z = L.z + b * zld;
-          R.k = k;
+          R.z = L.z;
+          R.k = (int32_t)(t * bpt);
           R.d = (int32_t)l.d;
           R.hb = (int32_t)hb;
           R.zld = zld;
           R.hdiv = L.hdiv;
+          R.ldx = (int32_t)l.ldx;
+          R.nblk = (int32_t)nblk;
+          R.nbt = (int32_t)(batch * nblk);
+          R.logh = __builtin_ctzll((unsigned long long)hb);
+          R.hrecip = 1.f / L.hdiv;
+        }
+      } else {
+        for (int64_t b = 0; b < batch; ++b) {
+          for (int k = 0; k < (int)(l.d / kRotTile); ++k) {
+            RotItem& R = items[z.n_rot_packed + rot_b++];
+            R.x = l.x + b * l.ldx;
+            R.rs = l.rot_scale;
+            R.z = L.z + b * zld;
+            R.k = k;
+            R.d = (int32_t)l.d;
+            R.hb = (int32_t)hb;
+            R.zld = zld;
+            R.hdiv = L.hdiv;
+            R.logh = __builtin_ctzll((unsigned long long)hb);
+            R.hrecip = 1.f / L.hdiv;
+          }
         }
       }
       zoff += zbuf_linear_bytes(batch, g.G4);
@@ -2017,15 +2212,19 @@ extern "C" int tp_stack_plan_init(const tp_stack_linear* linears, int n_linears,
     h->total_blocks = (int32_t)total;
     h->n_phases = z.n_phases;
     h->batch = (int32_t)batch;
-    h->n_rot = (int32_t)rot;
+    h->n_rot = (int32_t)(rot_p + rot_b);
+    h->n_rot_packed = (int32_t)rot_p;
     h->min_g4 = (int32_t)z.min_g4;
     h->zbuf_bytes = z.zbuf_bytes;
     if (hipMemcpy(plan, host, lay.zbuf, hipMemcpyHostToDevice) != hipSuccess) st = TP_ERR_HIP;
+    else if (z.zbuf_bytes && (hipMemset(zbuf, 0, (size_t)z.zbuf_bytes) != hipSuccess ||
+                              hipDeviceSynchronize() != hipSuccess))
+      st = TP_ERR_HIP;
   }
   {
     std::lock_guard<std::mutex> lock(g_plan_mutex);
     if (st == TP_OK && z.n_rot > 0)
-      g_plans[plan] = {(int)z.n_rot, (int)total, (int)batch, (int)total_k, big_rot, (int64_t)(lay.lin - kStackRO),
+      g_plans[plan] = {(int)rot_p, (int)rot_b, (int)total, (int)batch, (int)total_k, (int64_t)(lay.lin - kStackRO),
                        (int64_t)(lay.sched_o - kStackRO), (int64_t)(lay.sched_u - kStackRO)};
     else
       g_plans.erase(plan);
@@ -2040,18 +2239,16 @@ extern "C" int tp_stack_rotate(void* plan, int64_t batch, void* stream) {
   const char* ro = reinterpret_cast<const char*>(plan) + kStackRO;
   PlanReg reg;
   const bool known = plan_lookup(plan, &reg);
-  const int n_rot = known ? reg.n_rot : 0;
-  if (n_rot > 0) {
-    hipLaunchKernelGGL((tcq_stack_rotate_kernel<true, false>), dim3(n_rot), dim3(kRotThreads), 0,
-                       (hipStream_t)stream, ro);
-    if (reg.big_rot)
-      hipLaunchKernelGGL((tcq_stack_rotate_kernel<true, true>), dim3(n_rot), dim3(kRotThreads), 0,
-                         (hipStream_t)stream, ro);
+  hipStream_t s = (hipStream_t)stream;
+  if (known) {
+    if (reg.n_rot_packed > 0)
+      hipLaunchKernelGGL((tcq_stack_rotate_kernel<true>), dim3(reg.n_rot_packed), dim3(kRotThreads), 0, s, ro);
+    if (reg.n_rot_big > 0)
+      hipLaunchKernelGGL((tcq_stack_rotate_big_kernel<true>), dim3(reg.n_rot_big), dim3(kRotThreads), 0, s, ro);
   } else {
-    hipLaunchKernelGGL((tcq_stack_rotate_kernel<false, false>), dim3(2 * device_cu_count()), dim3(kRotThreads), 0,
-                       (hipStream_t)stream, ro);
-    hipLaunchKernelGGL((tcq_stack_rotate_kernel<false, true>), dim3(2 * device_cu_count()), dim3(kRotThreads), 0,
-                       (hipStream_t)stream, ro);
+    const int grid = 2 * device_cu_count();
+    hipLaunchKernelGGL((tcq_stack_rotate_kernel<false>), dim3(grid), dim3(kRotThreads), 0, s, ro);
+    hipLaunchKernelGGL((tcq_stack_rotate_big_kernel<false>), dim3(grid), dim3(kRotThreads), 0, s, ro);
   }
   return launch_status();
 }

@@ -61,17 +61,39 @@ __host__ __device__ constexpr int member_words(int bits) {
 
 // v / c, correctly rounded, for the fp32 c = sqrt(hb) of a power-of-two
 // block, from r = RN(1/c): q = RN(v r), then one correction step (Markstein:
-// e = v - q c is exact, RN(q + e r) is the rounded quotient).  Checked
-// against IEEE division for every fp32 v and every c = fp32(sqrt(2^j)),
-// j = 1..14: equal wherever |v / c| >= 2^-105 (below, the residual
-// underflows, and both quotients round to the same fp16 signed zero), given
-// that for v = -0 and +-inf q itself is the answer (the correction would
-// give +0 and NaN).
+// e = v - q c is exact, RN(q + e r) is the rounded quotient).  For v = +-0
+// and +-inf the correction gives +0 and NaN, so q itself is the answer
+// there.  Checked against IEEE division for every fp32 v and every
+// c = fp32(sqrt(2^j)), j = 1..14: equal wherever |v / c| >= 2^-105 (below,
+// the residual underflows, and both quotients round to the same fp16
+// signed zero).
 __device__ __forceinline__ float div_by_block_root(float v, float c, float r) {
   const float q = v * r;
   const float e = __builtin_fmaf(-q, c, v);
   const float q1 = __builtin_fmaf(e, r, q);
-  return __builtin_amdgcn_class(q, 0x264 /* -inf, -0, +0, +inf */) ? q : q1;
+  return __builtin_amdgcn_classf(q, 0x264 /* -inf, -0, +0, +inf */) ? q : q1;
+}
+
+// The same quotient with the special cases settled by v_div_fixup_f32
+// (one instruction instead of a class test and a select): the signed zero
+// for v = +-0, the signed infinity for v = +-inf, otherwise the corrected
+// quotient's magnitude with v's sign (its underflow clause needs
+// exponent(v) - exponent(c) < -150, impossible for c <= 2^23).  It keeps v
+// live to the end, which pushed one register-bound kernel into scratch; the
+// stack rotation uses it.
+__device__ __forceinline__ float div_by_block_root_fx(float v, float c, float r) {
+  const float q = v * r;
+  const float e = __builtin_fmaf(-q, c, v);
+  const float q1 = __builtin_fmaf(e, r, q);
+  return __builtin_amdgcn_div_fixupf(q1, c, v);
+}
+
+// Two fp32 values as two halves (low, high) of a word, each rounded to
+// nearest like f2h: one v_cvt_pk_f16_f32.
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  typedef float f2_t __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2_t{lo, hi}, h2_t));
 }
 
 // Lane xor 1, 2, 4 or 8 (inside a row of 16 lanes) with DPP moves: no LDS.
