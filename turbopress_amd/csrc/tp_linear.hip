@@ -28,6 +28,7 @@
 //     and leaves slices and counter zero.
 // The per-unit decode and MFMA step is the stack kernel's (tp_slot.h).
 #include "tp_slot.h"
+#include "tp_rotate_tile.h"
 
 namespace tp {
 
@@ -197,6 +198,76 @@ __device__ __forceinline__ void store4h(uint16_t* p, const float v[4]) {
   *reinterpret_cast<u32x2_t*>(p) = w;
 }
 
+// z of every batch row for blocks of 2^LOGH = 1024..4096 columns (the BIG
+// variants, which stage whole rows): each row's 4096-column tiles one after
+// the other (the last one partial when d is no multiple of 4096: its
+// missing columns are whole blocks, loaded as zeros and not stored), all 16
+// waves on a tile, four columns per thread: column 256 w + 4 m(l) + j of
+// the tile.  Butterflies at distance 1, 2 in registers, 4 .. 128 across
+// lanes (the lane stages of tp_rotate_tile.h), 256 .. 2048 across the
+// waves as radix-4 steps through `scr` (w bits 0, 1, then 2, 3) -- every
+// butterfly the reference's, in its order, so z is the reference's bit for
+// bit (and the same z as the stack rotation's).
+template <int LOGH>
+__device__ void lin_stage_big(const LinArgs& a, const LinPart& P, uint16_t* zl, float* scr, int wave, int lane) {
+  static_assert(LOGH >= 10 && LOGH <= 12, "blocks of 1024 .. 4096 columns");
+  const int tpr = (a.d + kRotTile - 1) / kRotTile;  // tiles per batch row
+  const int m = rot_lane_index(lane), lane4 = 4 * lane;
+  const int colw = 256 * wave + 4 * m;  // this thread's columns inside a tile
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(P.x, (uint32_t)((a.batch - 1) * P.ldx + a.d) * 2u);
+  const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(P.rs, (uint32_t)a.d * 2u);
+  const float c = a.hdiv, r = 1.f / c;
+  // radix-4 step over wave bits s, s + 1 (column distances 256 << s and
+  // 512 << s): u_k = the value of wave (w with those bits = k), then the
+  // natural-order H_4 row of this wave's two bits (distance 256 << s first)
+  auto radix4 = [&](float* v, int s) __attribute__((always_inline)) {
+    __syncthreads();  // earlier reads of scr are done
+    *reinterpret_cast<float4_t*>(scr + colw) = float4_t{v[0], v[1], v[2], v[3]};
+    __syncthreads();
+    const int base = colw - 256 * (wave & (3 << s));
+    const float s1 = ((wave >> s) & 1) ? -1.f : 1.f, s2 = ((wave >> (s + 1)) & 1) ? -1.f : 1.f;
+    const float4_t u0 = *reinterpret_cast<const float4_t*>(scr + base);
+    const float4_t u1 = *reinterpret_cast<const float4_t*>(scr + base + (256 << s));
+    const float4_t u2 = *reinterpret_cast<const float4_t*>(scr + base + (512 << s));
+    const float4_t u3 = *reinterpret_cast<const float4_t*>(scr + base + (768 << s));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float s01 = __builtin_fmaf(s1, u1[e], u0[e]);
+      const float s23 = __builtin_fmaf(s1, u3[e], u2[e]);
+      v[e] = __builtin_fmaf(s2, s23, s01);
+    }
+  };
+  for (int it = 0; it < a.batch * tpr; ++it) {
+    const int b = it / tpr;
+    const int col = (it - b * tpr) * kRotTile + colw;
+    const bool ok = col < a.d;
+    const u32x2_t xw = load4h_words(xrs, ok ? (uint32_t)(b * P.ldx + col) : kOutOfRange / 2u);
+    const u32x2_t rw = load4h_words(rrs, ok ? (uint32_t)col : kOutOfRange / 2u);
+    float v[4];
+    rot_products<true, 1>(&xw, &rw, v);
+    rot_reg_stage<2, 2, LOGH, 4>(v);
+    rot_lane_stage<0, LOGH, 4>(v, m, lane4);
+    rot_lane_stage<1, LOGH, 4>(v, m, lane4);
+    rot_lane_stage<2, LOGH, 4>(v, m, lane4);
+    rot_lane_stage<3, LOGH, 4>(v, m, lane4);
+    rot_lane_stage<4, LOGH, 4>(v, m, lane4);
+    rot_lane_stage<5, LOGH, 4>(v, m, lane4);
+    radix4(v, 0);  // distances 256, 512
+    if constexpr (LOGH == 11) {  // distance 1024: wave bit 2
+      __syncthreads();
+      *reinterpret_cast<float4_t*>(scr + colw) = float4_t{v[0], v[1], v[2], v[3]};
+      __syncthreads();
+      const float s1 = ((wave >> 2) & 1) ? -1.f : 1.f;
+      const float4_t p = *reinterpret_cast<const float4_t*>(scr + (colw ^ 1024));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = __builtin_fmaf(s1, v[e], p[e]);
+    } else if constexpr (LOGH == 12) {
+      radix4(v, 2);  // distances 1024, 2048
+    }
+    if (ok) *reinterpret_cast<u32x2_t*>(zl + b * a.zstride + col) = rot_z4<LOGH>(v, c, r);
+  }
+}
+
 // Stage z rows [0, batch) x columns [pu0 * 256, (pu0 + npu) * 256) of linear
 // P in LDS (column pu0 * 256 at LDS column 0; the BIG variant stages whole
 // rows: pu0 = 0, npu = G4).
@@ -243,77 +314,10 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>
     }
     return;
   } else {
-    const int m = a.hb / kChunkCols;  // 4, 8 or 16
-    for (int b = 0; b < a.batch; ++b) {
-      const uint16_t* xr = P.x + (size_t)b * P.ldx;
-      for (int ci = wave; ci < nch; ci += kLinWaves) {
-        const int c0 = ci * kChunkCols + lane * 4;
-        const int k = (ci - wave) / kLinWaves;  // prefetched item of row 0
-        float v[4];
-        if (pre && b == 0 && k < NPRE) {
-          // (k < NPRE is uniform: select the registers without indexing)
-          float t[4];
-#pragma unroll
-          for (int kk = 0; kk < NPRE; ++kk) {
-            if (kk == k) {
-              lin_pre_product(a, f, kk, ci * kChunkCols, t);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v[e] = t[e];
-            }
-          }
-        } else {
-          float xv[4], rv[4];
-          load4h(xr + c0, xv);
-          load4h(P.rs + c0, rv);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = xv[e] * rv[e];
-        }
-        float p = v[0], q = v[1];
-        v[0] = p + q; v[1] = p - q;
-        p = v[2]; q = v[3];
-        v[2] = p + q; v[3] = p - q;
-        p = v[0]; q = v[2];
-        v[0] = p + q; v[2] = p - q;
-        p = v[1]; q = v[3];
-        v[1] = p + q; v[3] = p - q;
-#pragma unroll
-        for (int sft = 0; sft < 6; ++sft) {
-          const bool upper = (lane >> sft) & 1;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float t = __shfl_xor(v[e], 1 << sft, 64);
-            v[e] = upper ? t - v[e] : v[e] + t;
-          }
-        }
-        *reinterpret_cast<float4_t*>(scr + c0) = float4_t{v[0], v[1], v[2], v[3]};
-      }
-      __syncthreads();
-      const int items = a.d / m;  // (block, position inside the chunk) pairs
-      for (int it = tid; it < items; it += kLinThreads) {
-        const int h = it / kChunkCols, pos = it - h * kChunkCols;
-        const int base = h * a.hb + pos;
-        float u[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) u[i] = i < m ? scr[base + i * kChunkCols] : 0.f;
-#pragma unroll
-        for (int dist = 1; dist < 16; dist <<= 1) {
-          if (dist < m) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              if (!(i & dist)) {
-                const float p = u[i], q = u[i + dist];
-                u[i] = p + q;
-                u[i + dist] = p - q;
-              }
-            }
-          }
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          if (i < m) zl[b * a.zstride + base + i * kChunkCols] = f2h(u[i] / a.hdiv);
-      }
-      __syncthreads();
-    }
+    const int logh = __builtin_ctz((unsigned)a.hb);  // 10, 11 or 12 (uniform)
+    if (logh == 10) lin_stage_big<10>(a, P, zl, scr, wave, lane);
+    else if (logh == 11) lin_stage_big<11>(a, P, zl, scr, wave, lane);
+    else lin_stage_big<12>(a, P, zl, scr, wave, lane);
   }
 }
 
@@ -419,7 +423,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     // rotation, which every decode waits for).
     const bool pre = ROT && key != staged && w == (int)blockIdx.x;
     XPre<lin_pre(KB)> xf;
-    if constexpr (ROT) {
+    if constexpr (ROT && !BIG) {
       if (pre) xf = lin_prefetch_x<lin_pre(KB)>(a, P, pu0, npu, wave, lane);
     }
 
