@@ -34,6 +34,20 @@ namespace tp {
 
 constexpr int kLinWaves = 16;
 constexpr int kLinThreads = 64 * kLinWaves;
+
+// x / d and x % d for wave-uniform 0 <= x < 8 d, d >= 1 (a batch row or a
+// wave's tile: a launch holds at most 8 batch rows): at most 7 scalar
+// subtractions, where a division is ~25 dependent instructions (a vector
+// reciprocal and its read-back) on the way to the first weight load.
+__device__ __forceinline__ int udiv_small(int x, int d, int* rem) {
+  int q = 0;
+  for (int i = 0; i < 7 && x >= d; ++i) {
+    x -= d;
+    ++q;
+  }
+  *rem = x;
+  return q;
+}
 // Units per wave, all loaded up front: 3, and 4 in launches of several
 // linears, where it lets two 9728-row linears (gate/up sharing their input)
 // fit one round of 244 workgroups (3 units: 304 workgroups on 256 CUs, two
@@ -120,9 +134,10 @@ __device__ __forceinline__ void lin_chunk_fwht(const LinArgs& a, int lane, float
 __device__ void lin_rotate_chunk(const LinArgs& a, const LinPart& P, int b, int cs, int lane, float v[4]) {
   const uint16_t* xr = P.x + (size_t)b * P.ldx;
   v[0] = v[1] = v[2] = v[3] = 0.f;
-  const int nsub = a.hb > kChunkCols ? a.hb / kChunkCols : 1;
-  const int base = a.hb > kChunkCols ? cs - cs % a.hb : cs;
-  const int o = a.hb > kChunkCols ? (cs % a.hb) / kChunkCols : 0;
+  // (hb is a power of two: masks and shifts)
+  const int nsub = a.hb > kChunkCols ? a.hb >> 8 : 1;
+  const int base = a.hb > kChunkCols ? cs & ~(a.hb - 1) : cs;
+  const int o = a.hb > kChunkCols ? (cs & (a.hb - 1)) >> 8 : 0;
   for (int i = 0; i < nsub; ++i) {
     const int c0 = base + i * kChunkCols + lane * 4;
     if (c0 < a.d) {  // d is a multiple of 4: a lane's group is wholly inside or outside
@@ -162,9 +177,10 @@ __device__ __forceinline__ XPre<NPRE> lin_prefetch_x(const LinArgs& a, const Lin
   for (int k = 0; k < NPRE; ++k) {
     const int it = wave + kLinWaves * k;
     const bool ok = it < items;
-    const int b = ok ? it / npu : 0;
-    const int cs = (pu0 + (ok ? it - b * npu : 0)) * kChunkCols;
-    const int base = (small && a.hb > kChunkCols) ? cs - cs % a.hb : cs;
+    int ci = 0;
+    const int b = ok ? udiv_small(it, npu, &ci) : 0;  // (it < batch * npu)
+    const int cs = (pu0 + ci) * kChunkCols;
+    const int base = (small && a.hb > kChunkCols) ? cs & ~(a.hb - 1) : cs;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int c0 = base + i * kChunkCols + lane * 4;
@@ -185,7 +201,7 @@ __device__ __forceinline__ void lin_pre_product(const LinArgs& a, const XPre<NPR
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[e] = 0.f + xv[e] * rv[e];
   if (a.hb > kChunkCols && a.hb <= 2 * kChunkCols) {
-    const bool neg = (cs % a.hb) != 0;  // second chunk of the block: row 1 of H_2
+    const bool neg = (cs & (a.hb - 1)) != 0;  // second chunk of the block: row 1 of H_2
     unpack4h(uint2{f.x[k][1][0], f.x[k][1][1]}, xv);
     unpack4h(uint2{f.r[k][1][0], f.r[k][1][1]}, rv);
 #pragma unroll
@@ -238,8 +254,9 @@ __device__ void lin_stage_big(const LinArgs& a, const LinPart& P, uint16_t* zl, 
     }
   };
   for (int it = 0; it < a.batch * tpr; ++it) {
-    const int b = it / tpr;
-    const int col = (it - b * tpr) * kRotTile + colw;
+    int tcol = 0;
+    const int b = udiv_small(it, tpr, &tcol);  // (it < batch * tpr)
+    const int col = tcol * kRotTile + colw;
     const bool ok = col < a.d;
     const u32x2_t xw = load4h_words(xrs, ok ? (uint32_t)(b * P.ldx + col) : kOutOfRange / 2u);
     const u32x2_t rw = load4h_words(rrs, ok ? (uint32_t)col : kOutOfRange / 2u);
@@ -297,7 +314,8 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>
       for (int k = 0; k < NPRE; ++k) {
         const int it = wave + kLinWaves * k;
         if (it < a.batch * nch) {
-          const int b = it / nch, ci = it - b * nch;
+          int ci = 0;
+          const int b = udiv_small(it, nch, &ci);  // (it < batch * nch)
           float v[4];
           lin_pre_product(a, f, k, (pu0 + ci) * kChunkCols, v);
           lin_chunk_fwht(a, lane, v);
@@ -307,7 +325,8 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>
       it0 = wave + kLinWaves * NPRE;
     }
     for (int it = it0; it < a.batch * nch; it += kLinWaves) {
-      const int b = it / nch, ci = it - b * nch;
+      int ci = 0;
+      const int b = udiv_small(it, nch, &ci);  // (it < batch * nch)
       float v[4];
       lin_rotate_chunk(a, P, b, (pu0 + ci) * kChunkCols, lane, v);
       store4h(zl + b * a.zstride + ci * kChunkCols + lane * 4, v);
@@ -380,8 +399,13 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   // batch read row 0: their MFMA columns are never written out).
   const int bbz = bb < a.batch ? bb : 0;
   const int zrow = bbz * a.zstride + q * kSegCols;
-  const int lt = wave / a.s;        // local tile of this wave
-  const int j = wave - lt * a.s;    // K chunk of this wave (inside the K part)
+  // (wave-uniform values are pinned to scalar registers: left to the
+  // compiler, the tile index reached the buffer descriptors as a vector
+  // value, and every weight load went into a waterfall loop)
+  int jw = 0;
+  const int ltw = a.s == 1 ? wave : udiv_small(wave, a.s, &jw);  // (wave < 16 <= 8 s for s >= 2)
+  const int lt = __builtin_amdgcn_readfirstlane(ltw);                    // local tile of this wave
+  const int j = __builtin_amdgcn_readfirstlane(a.s == 1 ? 0 : jw);       // K chunk of this wave (inside the K part)
   const uint32_t tile_p = (uint32_t)a.G4 * unit_p;  // path bytes of one tile
   const uint32_t tile_m = (uint32_t)a.G4 * unit_m;  // member bytes of one tile
   int staged = -1;
@@ -401,8 +425,8 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     }
     const int pu0 = KSPLIT ? kp * a.pu : 0;
     const int npu = KSPLIT ? min(a.pu, a.G4 - pu0) : a.G4;
-    const int u0 = pu0 + j * a.c;
-    const int nu = min(a.c, pu0 + npu - u0);
+    const int u0 = __builtin_amdgcn_readfirstlane(pu0 + j * a.c);
+    const int nu = __builtin_amdgcn_readfirstlane(min(a.c, pu0 + npu - u0));
     // The group's linear: the parts' first groups ascend and unused parts
     // start at `groups`, so it is the number of parts 1.. starting at or
     // before g.  (Computed from values of one argument round trip, then one
@@ -415,9 +439,9 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
       p = __builtin_amdgcn_readfirstlane(p);
     }
     const LinPart P = a.part[p];
-    const int t = (g - P.g0) * a.tpw + lt;
+    const int t = __builtin_amdgcn_readfirstlane((g - P.g0) * a.tpw + lt);
     const bool active = lt < a.tpw && t < P.T && nu > 0;  // wave-uniform
-    const int tt = active ? t : 0;
+    const int tt = __builtin_amdgcn_readfirstlane(active ? t : 0);
     const int key = p + kLinMaxParts * kp;  // what the LDS z holds
     // The first group's activations load before its weights (they gate the
     // rotation, which every decode waits for).

@@ -497,8 +497,13 @@ __device__ __forceinline__ UnitRegs<MW, NZ> stream_load(const SlotEnv& E, const 
   constexpr uint32_t unit_m = 4u * kTileRows * MW * 4u;   // member bytes per unit
   constexpr uint32_t unit_z = kChunkCols * 2u;            // z bytes per unit and batch row
   UnitRegs<MW, NZ> g;
-  g.X = __builtin_amdgcn_raw_buffer_load_b64(c.prs, E.pv, (uint32_t)gu * unit_p, weight_policy(MW));
-  g.M = MemberBuf<MW>::load(c.mrs, E.mv, (uint32_t)gu * unit_m);
+  // (at k=2 the unit index is pinned to a scalar register: left alone, the
+  // compiler kept it in a vector one there and put both weight loads into
+  // waterfall loops; at k=3 and 4 it stays scalar by itself, and the pin
+  // would cost a VALU instruction per unit)
+  const uint32_t ug = MW == 2 ? (uint32_t)__builtin_amdgcn_readfirstlane(gu) : (uint32_t)gu;
+  g.X = __builtin_amdgcn_raw_buffer_load_b64(c.prs, E.pv, ug * unit_p, weight_policy(MW));
+  g.M = MemberBuf<MW>::load(c.mrs, E.mv, ug * unit_m);
   // (uniform by construction; readfirstlane keeps it in a scalar register
   // when the compiler merges it with per-lane values)
   const uint32_t zs = (uint32_t)__builtin_amdgcn_readfirstlane((int)(c.zoff + (uint32_t)gu * unit_z));
