@@ -104,3 +104,33 @@ def test_shared_workspace_grows_and_retires(monkeypatch):
     assert hk.shared_workspace("cuda:0", 500) is a
     b = hk.shared_workspace("cuda:0", 5000)
     assert b.numel() == 5120 and hk._RETIRED_WORKSPACES == [a]
+
+
+def _lin_recip(d: int) -> int:
+    """The per-linear kernel's reciprocal for wave-uniform divisions
+    (``lin_recip`` in turbopress_amd/csrc/tp_linear.hip): ceil(2^32 / d),
+    0 standing for d = 1."""
+    return 0 if d <= 1 else -(-(1 << 32) // d)
+
+
+def test_reciprocal_division_is_exact_below_its_bound():
+    """udiv_recip(x, lin_recip(d)) = x // d whenever x * d < 2^32 (its
+    stated bound): every x < 2^16 for d <= 1024, and the largest x the bound
+    allows for d up to 2^16 (where a reciprocal rounded the other way, or a
+    bound one too loose, gives x // d + 1 or - 1)."""
+    import numpy as np
+
+    def udiv(x, d):
+        m = _lin_recip(d)
+        return x if m == 0 else (x.astype(np.uint64) * np.uint64(m)) >> np.uint64(32)
+
+    x = np.arange(1 << 16, dtype=np.uint64)
+    for d in range(1, 1025):
+        ok = x * np.uint64(d) < np.uint64(1 << 32)
+        assert np.array_equal(udiv(x[ok], d), x[ok] // np.uint64(d)), d
+    rng = np.random.default_rng(7)
+    for d in list(range(1025, 1100)) + [int(v) for v in rng.integers(1100, 1 << 16, 2000)]:
+        top = ((1 << 32) - 1) // d
+        xs = np.array([top, top - 1, top - d + 1, (top // d) * d, (top // d) * d - 1], dtype=np.uint64)
+        xs = xs[xs * np.uint64(d) < np.uint64(1 << 32)]
+        assert np.array_equal(udiv(xs, d), xs // np.uint64(d)), d

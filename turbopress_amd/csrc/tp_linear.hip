@@ -48,6 +48,17 @@ __device__ __forceinline__ int udiv_small(int x, int d, int* rem) {
   *rem = x;
   return q;
 }
+// x / d for wave-uniform x >= 0 with x * d < 2^32: one scalar multiply-high
+// by m = ceil(2^32 / d), which the host computes (lin_recip; m = 0 stands for
+// d = 1).  With x = q d + r, x m / 2^32 = q + r / d + x e / (d 2^32) for some
+// 0 <= e < d, and x e / (d 2^32) < x / 2^32 < 1 / d, so the floor is q.
+__device__ __forceinline__ int udiv_recip(int x, uint32_t m) {
+  return m ? (int)__umulhi((uint32_t)x, m) : x;
+}
+__host__ __device__ constexpr uint32_t lin_recip(int64_t d) {
+  return d <= 1 ? 0u : (uint32_t)(((int64_t)1 << 32) / d + (((int64_t)1 << 32) % d != 0));
+}
+
 // Units per wave, all loaded up front: 3, and 4 in launches of several
 // linears, where it lets two 9728-row linears (gate/up sharing their input)
 // fit one round of 244 workgroups (3 units: 304 workgroups on 256 CUs, two
@@ -81,18 +92,28 @@ struct LinPart {
   int32_t reserved;
 };
 
+// Every field a wave reads at its entry comes first, then part[0]: the
+// prologue's argument loads are then a few wide scalar loads of one span
+// instead of one per scattered field (each wave of a 16-wave workgroup makes
+// them, through one scalar cache).
 struct LinArgs {
-  LinPart part[kLinMaxParts];
   const uint16_t* codebook;
-  int32_t n_part, groups;    // tile groups over all linears
   int32_t d, G4, hb, batch;  // batch: rows of this launch (<= SB)
   int32_t c, s, tpw;         // units per chunk, chunks per tile, tiles per group
   int32_t zstride;           // halves per staged z row (units staged * 256 + 8: rows start 4 banks apart)
   float hdiv;                // sqrt(hb)
   int32_t kparts, pu;        // K parts per tile group (1: no split), units per part
+  int32_t n_part, groups;    // tile groups over all linears
+  int32_t g0[kLinMaxParts];  // part[i].g0: first tile group of each linear
+  uint32_t r_s, r_kparts;    // lin_recip(s), lin_recip(kparts)
+  uint32_t r_pu, r_pu_last;  // lin_recip of a K part's units: every part but the last, the last (or only) part
+  int32_t reserved;
+  LinPart part[kLinMaxParts];
   float* kws;                // K-split slices [kparts][T][16 rows][8] fp32 (zero between calls)
   uint32_t* kcnt;            // K-split arrival counter per row tile (zero between calls)
 };
+static_assert(sizeof(LinPart) == 80 && __builtin_offsetof(LinArgs, part) == 96,
+              "entry fields in the first 96 bytes, part[0] in the next 80");
 
 // Butterflies of one chunk (four columns per lane, lane-major) up to
 // distance min(hb, 256) / 2, then / sqrt(hb).
@@ -166,8 +187,8 @@ struct XPre {
 
 // Items of the K part [pu0, pu0 + npu) (units = 256-column chunks).
 template <int NPRE>
-__device__ __forceinline__ XPre<NPRE> lin_prefetch_x(const LinArgs& a, const LinPart& P, int pu0, int npu, int wave,
-                                                     int lane) {
+__device__ __forceinline__ XPre<NPRE> lin_prefetch_x(const LinArgs& a, const LinPart& P, int pu0, int npu,
+                                                     uint32_t rnpu, int wave, int lane) {
   XPre<NPRE> f;
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(P.x, (uint32_t)((a.batch - 1) * P.ldx + a.d) * 2u);
   const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(P.rs, (uint32_t)a.d * 2u);
@@ -177,8 +198,8 @@ __device__ __forceinline__ XPre<NPRE> lin_prefetch_x(const LinArgs& a, const Lin
   for (int k = 0; k < NPRE; ++k) {
     const int it = wave + kLinWaves * k;
     const bool ok = it < items;
-    int ci = 0;
-    const int b = ok ? udiv_small(it, npu, &ci) : 0;  // (it < batch * npu)
+    const int b = ok ? udiv_recip(it, rnpu) : 0;  // (it < batch * npu)
+    const int ci = ok ? it - b * npu : 0;
     const int cs = (pu0 + ci) * kChunkCols;
     const int base = (small && a.hb > kChunkCols) ? cs & ~(a.hb - 1) : cs;
 #pragma unroll
@@ -296,7 +317,7 @@ __device__ void lin_stage_big(const LinArgs& a, const LinPart& P, uint16_t* zl, 
 // holds that path's registers); the others take blocks <= 512 only.
 template <bool ROT, bool BIG, int NPRE>
 __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>& f, bool pre, int pu0, int npu,
-                            uint16_t* zl, float* scr, int tid, int wave, int lane) {
+                            uint32_t rnpu, uint16_t* zl, float* scr, int tid, int wave, int lane) {
   const int nch = npu;
   if constexpr (!ROT) {
     const int per_row = nch * kChunkCols / 8;
@@ -314,8 +335,8 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>
       for (int k = 0; k < NPRE; ++k) {
         const int it = wave + kLinWaves * k;
         if (it < a.batch * nch) {
-          int ci = 0;
-          const int b = udiv_small(it, nch, &ci);  // (it < batch * nch)
+          const int b = udiv_recip(it, rnpu);  // (it < batch * nch)
+          const int ci = it - b * nch;
           float v[4];
           lin_pre_product(a, f, k, (pu0 + ci) * kChunkCols, v);
           lin_chunk_fwht(a, lane, v);
@@ -325,8 +346,8 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>
       it0 = wave + kLinWaves * NPRE;
     }
     for (int it = it0; it < a.batch * nch; it += kLinWaves) {
-      int ci = 0;
-      const int b = udiv_small(it, nch, &ci);  // (it < batch * nch)
+      const int b = udiv_recip(it, rnpu);  // (it < batch * nch)
+      const int ci = it - b * nch;
       float v[4];
       lin_rotate_chunk(a, P, b, (pu0 + ci) * kChunkCols, lane, v);
       store4h(zl + b * a.zstride + ci * kChunkCols + lane * 4, v);
@@ -368,18 +389,20 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   if constexpr (BIG) {
   } else if constexpr (MULTI) {
     __asm__ volatile("" ::"s"(codebook), "s"(a.d), "s"(a.hb), "s"(a.batch), "s"(a.tpw), "s"(a.zstride),
-                     "s"(a.hdiv), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(a.part[1].g0), "s"(a.part[2].g0),
-                     "s"(a.part[3].g0)
+                     "s"(a.hdiv), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(a.g0[1]), "s"(a.g0[2]),
+                     "s"(a.g0[3]), "s"(a.r_s), "s"(a.r_pu_last)
                      : "memory");
   } else if constexpr (KSPLIT) {
     const LinPart& P0 = a.part[0];
-    __asm__ volatile("" ::"s"(codebook), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(a.kparts), "s"(a.pu), "s"(P0.path),
-                     "s"(P0.member), "s"(P0.x), "s"(P0.rs)
+    __asm__ volatile("" ::"s"(codebook), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(a.kparts), "s"(a.pu), "s"(a.r_s),
+                     "s"(a.r_kparts), "s"(a.r_pu), "s"(a.r_pu_last), "s"(P0.path), "s"(P0.member), "s"(P0.x),
+                     "s"(P0.rs)
                      : "memory");
   } else {
     const LinPart& P0 = a.part[0];
     __asm__ volatile("" ::"s"(codebook), "s"(a.d), "s"(a.hb), "s"(a.batch), "s"(a.tpw), "s"(a.zstride),
-                     "s"(a.hdiv), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(P0.path), "s"(P0.member), "s"(P0.x),
+                     "s"(a.hdiv), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(a.r_s), "s"(a.r_pu_last), "s"(P0.path),
+                     "s"(P0.member), "s"(P0.x),
                      "s"(P0.rs), "s"(P0.scales), "s"(P0.n), "s"(P0.T), "s"(P0.g0)
                      : "memory");
   }
@@ -402,10 +425,8 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   // (wave-uniform values are pinned to scalar registers: left to the
   // compiler, the tile index reached the buffer descriptors as a vector
   // value, and every weight load went into a waterfall loop)
-  int jw = 0;
-  const int ltw = a.s == 1 ? wave : udiv_small(wave, a.s, &jw);  // (wave < 16 <= 8 s for s >= 2)
-  const int lt = __builtin_amdgcn_readfirstlane(ltw);                    // local tile of this wave
-  const int j = __builtin_amdgcn_readfirstlane(a.s == 1 ? 0 : jw);       // K chunk of this wave (inside the K part)
+  const int lt = __builtin_amdgcn_readfirstlane(udiv_recip(wave, a.r_s));  // local tile of this wave
+  const int j = __builtin_amdgcn_readfirstlane(wave - lt * a.s);            // K chunk of this wave (inside the K part)
   const uint32_t tile_p = (uint32_t)a.G4 * unit_p;  // path bytes of one tile
   const uint32_t tile_m = (uint32_t)a.G4 * unit_m;  // member bytes of one tile
   int staged = -1;
@@ -420,11 +441,12 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     // Work item w: tile group g, K part kp of units [pu0, pu0 + npu).
     int g = w, kp = 0;
     if constexpr (KSPLIT) {
-      g = w / a.kparts;
+      g = udiv_recip(w, a.r_kparts);
       kp = w - g * a.kparts;
     }
     const int pu0 = KSPLIT ? kp * a.pu : 0;
     const int npu = KSPLIT ? min(a.pu, a.G4 - pu0) : a.G4;
+    const uint32_t rnpu = (KSPLIT && kp + 1 < a.kparts) ? a.r_pu : a.r_pu_last;
     const int u0 = __builtin_amdgcn_readfirstlane(pu0 + j * a.c);
     const int nu = __builtin_amdgcn_readfirstlane(min(a.c, pu0 + npu - u0));
     // The group's linear: the parts' first groups ascend and unused parts
@@ -435,7 +457,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     int p = 0;
     if constexpr (MULTI) {
 #pragma unroll
-      for (int i = 1; i < kLinMaxParts; ++i) p += g >= a.part[i].g0 ? 1 : 0;
+      for (int i = 1; i < kLinMaxParts; ++i) p += g >= a.g0[i] ? 1 : 0;
       p = __builtin_amdgcn_readfirstlane(p);
     }
     const LinPart P = a.part[p];
@@ -448,21 +470,26 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     const bool pre = ROT && key != staged && w == (int)blockIdx.x;
     XPre<lin_pre(KB)> xf;
     if constexpr (ROT && !BIG) {
-      if (pre) xf = lin_prefetch_x<lin_pre(KB)>(a, P, pu0, npu, wave, lane);
+      if (pre) xf = lin_prefetch_x<lin_pre(KB)>(a, P, pu0, npu, rnpu, wave, lane);
     }
 
     // Every weight load of this wave, then the halo word (path word 1 of
     // the unit before the chunk, K block 3 lanes) and the row scales.
-    const __amdgpu_buffer_rsrc_t prs = buffer_rsrc(reinterpret_cast<const char*>(P.path) + (size_t)tt * tile_p, tile_p);
-    const __amdgpu_buffer_rsrc_t mrs = buffer_rsrc(reinterpret_cast<const char*>(P.member) + (size_t)tt * tile_m, tile_m);
+    const __amdgpu_buffer_rsrc_t prs =
+        buffer_rsrc(reinterpret_cast<const char*>(P.path) + (size_t)(uint32_t)tt * tile_p, tile_p);
+    const __amdgpu_buffer_rsrc_t mrs =
+        buffer_rsrc(reinterpret_cast<const char*>(P.member) + (size_t)(uint32_t)tt * tile_m, tile_m);
     constexpr int MAXU = lin_max_units(MULTI);
     UnitRegs<MW, NZ> R[MAXU];
+    // (a unit past the wave's range loads out of range: the vector offset
+    // carries the out-of-range bit, so its scalar offset needs no select;
+    // the range check fails whatever that offset, which stays below 2^31)
+    const uint32_t su0 = (uint32_t)u0;
 #pragma unroll
     for (int u = 0; u < MAXU; ++u) {
-      const bool ok = active && u < nu;
-      const uint32_t gu = (uint32_t)(ok ? u0 + u : 0);
-      R[u].X = __builtin_amdgcn_raw_buffer_load_b64(prs, ok ? pv : kOutOfRange, gu * unit_p, weight_policy(MW));
-      R[u].M = MemberBuf<MW>::load(mrs, ok ? mv : kOutOfRange, gu * unit_m);
+      const uint32_t oob = (active && u < nu) ? 0u : kOutOfRange;  // (wave-uniform)
+      R[u].X = __builtin_amdgcn_raw_buffer_load_b64(prs, pv | oob, (su0 + u) * unit_p, weight_policy(MW));
+      R[u].M = MemberBuf<MW>::load(mrs, mv | oob, (su0 + u) * unit_m);
     }
     const uint32_t x1_prev = __builtin_amdgcn_raw_buffer_load_b32(
         prs, (active && u0 > 0) ? pv + 4u : kOutOfRange, (uint32_t)(u0 > 0 ? u0 - 1 : 0) * unit_p, 0);
@@ -474,7 +501,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     if (w == (int)blockIdx.x) build_pair_table_lanes<KB>(table, cb_lane, tid, kLinThreads);
     if (key != staged) {
       if (staged >= 0) __syncthreads();  // the previous group's reads of z and scr are done
-      lin_stage_z<ROT, BIG, lin_pre(KB)>(a, P, xf, pre, pu0, npu, zl, scr, tid, wave, lane);
+      lin_stage_z<ROT, BIG, lin_pre(KB)>(a, P, xf, pre, pu0, npu, rnpu, zl, scr, tid, wave, lane);
       staged = key;
     }
     __syncthreads();
@@ -757,6 +784,11 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   const LinPlan best = plan_linear(n_lin, T, G4, d, hb, rot, batch, bits, ws_ok,
                                    ws_ok ? ls[0].workspace_bytes : 0, cus, (int64_t)device_max_lds());
   if (best.kparts == 0) return kLinearNotHandled;
+  // (the kernel's divisions by reciprocal need x * d < 2^32: work items x
+  // K parts; its unit offsets stay below 2^31 up to the last unit loaded)
+  if (best.groups * best.kparts * best.kparts >= ((int64_t)1 << 32) ||
+      (G4 + kLinMaxUnitsMulti) * (4 * kTileRows * member_words(bits) * 4) >= ((int64_t)1 << 31))
+    return kLinearNotHandled;
 
   const int64_t zstride = best.pu * kChunkCols + 8;
   const int64_t scr = std::max<int64_t>(kLinRedBytes, big ? d * 4 : 0);
@@ -775,8 +807,13 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   a.hdiv = (float)__builtin_sqrt((double)hb);
   a.kparts = (int32_t)best.kparts;
   a.pu = (int32_t)best.pu;
+  a.r_s = lin_recip(best.sc);
+  a.r_kparts = lin_recip(best.kparts);
+  a.r_pu = lin_recip(best.pu);
+  a.r_pu_last = lin_recip(G4 - (best.kparts - 1) * best.pu);
   a.kws = nullptr;
   a.kcnt = nullptr;
+  a.reserved = 0;
   int64_t g0acc = 0;
   for (int i = 0; i < kLinMaxParts; ++i) {
     const TiledLinearArgs& l = ls[i < n_lin ? i : 0];
@@ -792,6 +829,7 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
     P.ldy = (int32_t)l.ldy;
     P.g0 = (int32_t)(i < n_lin ? g0acc : best.groups);
     P.reserved = 0;
+    a.g0[i] = P.g0;
     if (i < n_lin) g0acc += (T[i] + best.tpw - 1) / best.tpw;
   }
   if (best.kparts > 1) {
