@@ -107,25 +107,29 @@ struct LinArgs {
   int32_t g0[kLinMaxParts];  // part[i].g0: first tile group of each linear
   uint32_t r_s, r_kparts;    // lin_recip(s), lin_recip(kparts)
   uint32_t r_pu, r_pu_last;  // lin_recip of a K part's units: every part but the last, the last (or only) part
+  uint32_t r_batch;          // lin_recip(batch)
+  int32_t sk, sk_last;       // chunks of c units in a K part: every part but the last, the last (or only) part
   int32_t reserved;
   LinPart part[kLinMaxParts];
   float* kws;                // K-split slices [kparts][T][16 rows][8] fp32 (zero between calls)
   uint32_t* kcnt;            // K-split arrival counter per row tile (zero between calls)
 };
-static_assert(sizeof(LinPart) == 80 && __builtin_offsetof(LinArgs, part) == 96,
-              "entry fields in the first 96 bytes, part[0] in the next 80");
+static_assert(sizeof(LinPart) == 80 && __builtin_offsetof(LinArgs, part) == 112,
+              "entry fields in the first 112 bytes, then part[0]");
 
 // Butterflies of one chunk (four columns per lane, lane-major) up to
-// distance min(hb, 256) / 2, then / sqrt(hb).
-__device__ __forceinline__ void lin_chunk_fwht(const LinArgs& a, int lane, float v[4]) {
-  const int hmax = a.hb < kChunkCols ? a.hb : kChunkCols;
-  if (hmax > 1) {
+// distance hmax / 2.  FULL: hmax = 256, every stage (no stage test: each
+// test is a few scalar instructions per staged chunk, and the 16 waves of a
+// workgroup share one scalar unit).
+template <bool FULL>
+__device__ __forceinline__ void lin_chunk_stages(int hmax, int lane, float v[4]) {
+  if (FULL || hmax > 1) {
     float p = v[0], q = v[1];
     v[0] = p + q; v[1] = p - q;
     p = v[2]; q = v[3];
     v[2] = p + q; v[3] = p - q;
   }
-  if (hmax > 2) {
+  if (FULL || hmax > 2) {
     float p = v[0], q = v[2];
     v[0] = p + q; v[2] = p - q;
     p = v[1]; q = v[3];
@@ -134,7 +138,7 @@ __device__ __forceinline__ void lin_chunk_fwht(const LinArgs& a, int lane, float
   // (the upper lane of a pair keeps p - v: one FMA with the lane's sign)
 #pragma unroll
   for (int sft = 0; sft < 6; ++sft) {
-    if ((4 << sft) < hmax) {
+    if (FULL || (4 << sft) < hmax) {
       const float sg = ((lane >> sft) & 1) ? -1.f : 1.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -143,6 +147,12 @@ __device__ __forceinline__ void lin_chunk_fwht(const LinArgs& a, int lane, float
       }
     }
   }
+}
+
+// Butterflies of one chunk up to distance min(hb, 256) / 2, then / sqrt(hb).
+__device__ __forceinline__ void lin_chunk_fwht(const LinArgs& a, int lane, float v[4]) {
+  if (a.hb >= kChunkCols) lin_chunk_stages<true>(kChunkCols, lane, v);
+  else lin_chunk_stages<false>(a.hb, lane, v);
   const float r = 1.f / a.hdiv;
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[e] = div_by_block_root(v[e], a.hdiv, r);
@@ -485,9 +495,11 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     // carries the out-of-range bit, so its scalar offset needs no select;
     // the range check fails whatever that offset, which stays below 2^31)
     const uint32_t su0 = (uint32_t)u0;
+    const int lim = active ? nu : 0;  // units of this wave that load (wave-uniform)
 #pragma unroll
     for (int u = 0; u < MAXU; ++u) {
-      const uint32_t oob = (active && u < nu) ? 0u : kOutOfRange;  // (wave-uniform)
+      // out-of-range bit unless u < lim: the sign of lim - u - 1 (|lim| <= 4)
+      const uint32_t oob = (uint32_t)(lim - u - 1) & kOutOfRange;
       R[u].X = __builtin_amdgcn_raw_buffer_load_b64(prs, pv | oob, (su0 + u) * unit_p, weight_policy(MW));
       R[u].M = MemberBuf<MW>::load(mrs, mv | oob, (su0 + u) * unit_m);
     }
@@ -495,8 +507,9 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
         prs, (active && u0 > 0) ? pv + 4u : kOutOfRange, (uint32_t)(u0 > 0 ? u0 - 1 : 0) * unit_p, 0);
     const __amdgpu_buffer_rsrc_t srs = buffer_rsrc(P.scales, (uint32_t)P.n * 2u);
     // rows 4q..4q+3 (zero past n; for odd n also row n - 1, which shares its
-    // dword with row n: the epilogue reads that row again)
+    // dword with row n: loaded again on its own, and taken for that row)
     const u32x2_t sc = __builtin_amdgcn_raw_buffer_load_b64(srs, (uint32_t)(tt * kTileRows + 4 * q) * 2u, 0, 0);
+    const uint16_t sc_last = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(srs, (uint32_t)(P.n - 1) * 2u, 0, 0);
 
     if (w == (int)blockIdx.x) build_pair_table_lanes<KB>(table, cb_lane, tid, kLinThreads);
     if (key != staged) {
@@ -541,7 +554,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     if (active && j == 0) {
       float4_t v = *reinterpret_cast<const float4_t*>(scr + (wave * 64 + lane) * 4);
       // (chunks of this part that hold units: a short last part has fewer)
-      const int sk = KSPLIT ? (npu + a.c - 1) / a.c : a.s;
+      const int sk = KSPLIT ? (kp + 1 < a.kparts ? a.sk : a.sk_last) : a.s;
       for (int k = 1; k < sk; ++k) {
         const float4_t o = *reinterpret_cast<const float4_t*>(scr + ((wave + k) * 64 + lane) * 4);
 #pragma unroll
@@ -580,7 +593,8 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
             for (int h = 0; h < 2; ++h) {
               const int e = lane + 64 * h;
               if (e < ne) {
-                const int row = e / a.batch, col = e - row * a.batch;
+                const int row = a.r_batch ? (int)__umulhi((uint32_t)e, a.r_batch) : e;  // e / batch
+                const int col = e - row * a.batch;
                 const int grow = t * kTileRows + row;
                 const uint32_t off = ((uint32_t)t * kLinSliceFloats + (uint32_t)(row * 8 + col)) * 4u;
                 const uint16_t sv = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
@@ -616,8 +630,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
         for (int i = 0; i < 4; ++i) {
           const int row = row0 + i;
           if (row >= P.n) continue;
-          uint16_t sv = (uint16_t)(sc[i >> 1] >> (16 * (i & 1)));
-          if ((P.n & 1) && row == P.n - 1) sv = gld(P.scales + row);
+          const uint16_t sv = row == P.n - 1 ? sc_last : (uint16_t)(sc[i >> 1] >> (16 * (i & 1)));
           uint16_t out = f2h(v[i] * h2f(sv));
           if (P.bias) out = f2h(h2f(out) + h2f(gld(P.bias + row)));
           gst(P.y + (size_t)bb * P.ldy + row, out);
@@ -811,6 +824,8 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   a.r_kparts = lin_recip(best.kparts);
   a.r_pu = lin_recip(best.pu);
   a.r_pu_last = lin_recip(G4 - (best.kparts - 1) * best.pu);
+  a.sk = (int32_t)((best.pu + best.c - 1) / best.c);
+  a.sk_last = (int32_t)((G4 - (best.kparts - 1) * best.pu + best.c - 1) / best.c);
   a.kws = nullptr;
   a.kcnt = nullptr;
   a.reserved = 0;
@@ -844,6 +859,7 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   const int64_t work = best.groups * best.kparts;
   const int grid = (int)std::min<int64_t>(work, cus);
   a.batch = (int32_t)batch;
+  a.r_batch = lin_recip(batch);
   for (int i = 0; i < kLinMaxParts; ++i) {
     const TiledLinearArgs& l = ls[i < n_lin ? i : 0];
     a.part[i].x = l.x;
