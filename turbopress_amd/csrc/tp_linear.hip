@@ -203,21 +203,38 @@ __device__ __forceinline__ XPre<NPRE> lin_prefetch_x(const LinArgs& a, const Lin
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(P.x, (uint32_t)((a.batch - 1) * P.ldx + a.d) * 2u);
   const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(P.rs, (uint32_t)a.d * 2u);
   const bool small = a.hb <= 2 * kChunkCols;
+  const bool pair = small && a.hb > kChunkCols;  // a 512-block: both of its chunks
   const int items = (small ? a.batch : 1) * npu;
+  // (items past the count, and the second chunk unless pair, are not loaded
+  // at all -- wave-uniform branches: out-of-range loads still take their
+  // turn in the workgroup's vector memory path, which the 16 waves' prologue
+  // loads queue on; the staging reads only the items it loaded)
 #pragma unroll
   for (int k = 0; k < NPRE; ++k) {
     const int it = wave + kLinWaves * k;
-    const bool ok = it < items;
-    const int b = ok ? udiv_recip(it, rnpu) : 0;  // (it < batch * npu)
-    const int ci = ok ? it - b * npu : 0;
-    const int cs = (pu0 + ci) * kChunkCols;
-    const int base = (small && a.hb > kChunkCols) ? cs & ~(a.hb - 1) : cs;
+    if (it < items) {
+      const int b = udiv_recip(it, rnpu);  // (it < batch * npu)
+      const int ci = it - b * npu;
+      const int cs = (pu0 + ci) * kChunkCols;
+      const int base = pair ? cs & ~(a.hb - 1) : cs;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c0 = base + i * kChunkCols + lane * 4;
-      const bool in = ok && (i == 0 || (small && a.hb > kChunkCols)) && c0 < a.d;
-      f.x[k][i] = __builtin_amdgcn_raw_buffer_load_b64(xrs, in ? (uint32_t)(b * P.ldx + c0) * 2u : kOutOfRange, 0, 0);
-      f.r[k][i] = __builtin_amdgcn_raw_buffer_load_b64(rrs, in ? (uint32_t)c0 * 2u : kOutOfRange, 0, 0);
+      for (int i = 0; i < 2; ++i) {
+        if (i == 0 || pair) {
+          const int c0 = base + i * kChunkCols + lane * 4;
+          const bool in = c0 < a.d;
+          f.x[k][i] = __builtin_amdgcn_raw_buffer_load_b64(xrs, in ? (uint32_t)(b * P.ldx + c0) * 2u : kOutOfRange, 0, 0);
+          f.r[k][i] = __builtin_amdgcn_raw_buffer_load_b64(rrs, in ? (uint32_t)c0 * 2u : kOutOfRange, 0, 0);
+        } else {
+          f.x[k][i] = u32x2_t{0u, 0u};
+          f.r[k][i] = u32x2_t{0u, 0u};
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        f.x[k][i] = u32x2_t{0u, 0u};
+        f.r[k][i] = u32x2_t{0u, 0u};
+      }
     }
   }
   return f;
@@ -391,10 +408,9 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   // memory clobber keeps the loads below it).  Left to the compiler, the
   // codebook entry's load went first and its address wait held back the
   // other argument loads, and a multi-linear launch chained one round trip
-  // per part: each ~1-2 us before the first weight load.  The codebook
-  // entry is then the first vector load in flight (see cb_lane).  Not in
-  // the BIG variants: there the forced loads spilled scalar registers and
-  // the launch got slower (c1 q_proj 8.4 -> 8.7 us).
+  // per part: each ~1-2 us before the first weight load.  Not in the BIG
+  // variants: there the forced loads spilled scalar registers and the
+  // launch got slower (c1 q_proj 8.4 -> 8.7 us).
   const uint16_t* const codebook = a.codebook;
   if constexpr (BIG) {
   } else if constexpr (MULTI) {
@@ -440,7 +456,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   const uint32_t tile_p = (uint32_t)a.G4 * unit_p;  // path bytes of one tile
   const uint32_t tile_m = (uint32_t)a.G4 * unit_m;  // member bytes of one tile
   int staged = -1;
-  const uint32_t cb_lane = gld(codebook + (lane & ((2 << KB) - 1)));
+  const uint32_t cb_lane = codebook_lane_scalar<KB>(codebook, lane);  // (no vector load: see there)
 
   // One tile group.  The first call (the workgroup's own group; the host
   // gives every workgroup one group when they fit) is a copy of its own, so
@@ -491,11 +507,14 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
         buffer_rsrc(reinterpret_cast<const char*>(P.member) + (size_t)(uint32_t)tt * tile_m, tile_m);
     constexpr int MAXU = lin_max_units(MULTI);
     UnitRegs<MW, NZ> R[MAXU];
-    // (a unit past the wave's range loads out of range: the vector offset
-    // carries the out-of-range bit, so its scalar offset needs no select;
-    // the range check fails whatever that offset, which stays below 2^31)
     const uint32_t su0 = (uint32_t)u0;
     const int lim = active ? nu : 0;  // units of this wave that load (wave-uniform)
+    // (every unit is loaded, past lim out of range: the vector offset
+    // carries the out-of-range bit, so the scalar offset needs no select --
+    // the range check fails whatever that offset, which stays below 2^31.
+    // Unconditional, so that the number of loads issued after the
+    // activation prefetch is the same on every path and the staging's wait
+    // for the prefetch does not also wait for these)
 #pragma unroll
     for (int u = 0; u < MAXU; ++u) {
       // out-of-range bit unless u < lim: the sign of lim - u - 1 (|lim| <= 4)
@@ -775,6 +794,7 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
                         int bits, int n_states, hipStream_t s, bool clear_ws) {
   if (batch < 1 || batch > 8 || n_lin < 1 || n_lin > kLinMaxParts) return kLinearNotHandled;
   if (bits < 2 || bits > 4) return kLinearNotHandled;
+  if ((uintptr_t)codebook & 3) return kLinearNotHandled;  // (read as dwords through the scalar cache)
   const bool rot = ls[0].rot_scale != nullptr;
   const int64_t d = ls[0].d, hb = rot ? ls[0].block : 1;
   for (int i = 1; i < n_lin; ++i)

@@ -130,11 +130,8 @@ constexpr int kOrdLineWords = 32;
 constexpr size_t kStackRO = sizeof(StackCounters);
 constexpr size_t kRotItems = (kStackRO + sizeof(StackInfo) + 63) & ~(size_t)63;  // fixed offset
 
-// Reads of the plan's read-only part through the constant address space:
-// the plan does not change during a launch, so wave-uniform reads become
-// scalar loads (a vector load would make every value derived from it
-// per-lane, and its wait would also drain the weight loads in flight).
-#define TP_CONST __attribute__((address_space(4)))
+// Reads of the plan's read-only part through the constant address space
+// (TP_CONST): the plan does not change during a launch.
 template <typename T>
 __device__ __forceinline__ const TP_CONST T& cread(const T* p) {
   return *(const TP_CONST T*)p;
@@ -594,26 +591,8 @@ __device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1
   for (int k = 0; k < D - 1; ++k) TP_STREAM_ISSUE(k);
   // The pair table, built while the first units' loads are in flight: built
   // first, it held every first weight load ~2 us behind the launch's start.
-  // The codebook comes through the scalar cache (2^KB dwords, 4-byte
-  // aligned), so the build waits for no vector load: a lane's entry is
-  // picked from the scalar registers.
-  {
-    constexpr int NW = 1 << KB;  // dwords of 2^(KB+1) fp16 entries
-    const TP_CONST uint32_t* cbw = (const TP_CONST uint32_t*)codebook;
-    uint32_t w[NW];
-#pragma unroll
-    for (int i = 0; i < NW; ++i) {
-      w[i] = cbw[i];
-      // (kept a scalar value: else a select between two of them became a
-      // per-lane vector load, whose wait drained the weight loads)
-      __asm__ volatile("" : "+s"(w[i]));
-    }
-    const int e = E.lane & (2 * NW - 1);
-    uint32_t v = w[0];
-#pragma unroll
-    for (int i = 1; i < NW; ++i) v = (e >> 1) == i ? w[i] : v;
-    build_pair_table_lanes<KB>(table, (e & 1) ? v >> 16 : v & 0xFFFFu, E.tid, kGroupThreads);
-  }
+  // The codebook comes through the scalar cache (codebook_lane_scalar).
+  build_pair_table_lanes<KB>(table, codebook_lane_scalar<KB>(codebook, E.lane), E.tid, kGroupThreads);
   __syncthreads();
 
   for (;;) {

@@ -338,6 +338,37 @@ __device__ void build_pair_table(uint32_t* table, const uint16_t* cb, int tid, i
   }
 }
 
+// Reads through the constant address space: data a launch does not change,
+// read at wave-uniform addresses, become scalar loads (a vector load would
+// make every value derived from it per-lane, and its wait would also drain
+// the weight loads in flight).
+#define TP_CONST __attribute__((address_space(4)))
+
+// This lane's codebook entry (cb[lane % 2^(KB+1)], the input of
+// build_pair_table_lanes) through the scalar cache: the 2^(KB+1) fp16 entries
+// are 2^KB dwords of a 4-byte aligned codebook, and the lane's entry is
+// picked from scalar registers, so the table build waits for no vector load
+// (the vector memory counter is in order: waiting for a load issued at the
+// launch's start would also wait for every load issued after it).
+template <int KB>
+__device__ __forceinline__ uint32_t codebook_lane_scalar(const uint16_t* codebook, int lane) {
+  constexpr int NW = 1 << KB;  // dwords of 2^(KB+1) fp16 entries
+  const TP_CONST uint32_t* cbw = (const TP_CONST uint32_t*)codebook;
+  uint32_t w[NW];
+#pragma unroll
+  for (int i = 0; i < NW; ++i) {
+    w[i] = cbw[i];
+    // (kept a scalar value: else a select between two of them became a
+    // per-lane vector load)
+    __asm__ volatile("" : "+s"(w[i]));
+  }
+  const int e = lane & (2 * NW - 1);
+  uint32_t v = w[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) v = (e >> 1) == i ? w[i] : v;
+  return (e & 1) ? v >> 16 : v & 0xFFFFu;
+}
+
 // Same table from a codebook held one entry per lane (lane l has cb[l % 2^(KB+1)]):
 // no memory reads, entries gathered with lane shuffles.
 template <int KB>
