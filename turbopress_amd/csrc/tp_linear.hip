@@ -420,9 +420,11 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
                      : "memory");
   } else if constexpr (KSPLIT) {
     const LinPart& P0 = a.part[0];
-    __asm__ volatile("" ::"s"(codebook), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(a.kparts), "s"(a.pu), "s"(a.r_s),
-                     "s"(a.r_kparts), "s"(a.r_pu), "s"(a.r_pu_last), "s"(P0.path), "s"(P0.member), "s"(P0.x),
-                     "s"(P0.rs)
+    __asm__ volatile("" ::"s"(codebook), "s"(a.d), "s"(a.hb), "s"(a.batch), "s"(a.tpw), "s"(a.zstride),
+                     "s"(a.hdiv), "s"(a.G4), "s"(a.c), "s"(a.s), "s"(a.kparts), "s"(a.pu), "s"(a.groups),
+                     "s"(a.r_s), "s"(a.r_kparts), "s"(a.r_pu), "s"(a.r_pu_last), "s"(P0.path), "s"(P0.member),
+                     "s"(P0.x), "s"(P0.rs), "s"(P0.scales), "s"(P0.n), "s"(P0.T), "s"(P0.ldx), "s"(a.kws),
+                     "s"(a.kcnt)
                      : "memory");
   } else {
     const LinPart& P0 = a.part[0];
@@ -456,7 +458,6 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   const uint32_t tile_p = (uint32_t)a.G4 * unit_p;  // path bytes of one tile
   const uint32_t tile_m = (uint32_t)a.G4 * unit_m;  // member bytes of one tile
   int staged = -1;
-  const uint32_t cb_lane = codebook_lane_scalar<KB>(codebook, lane);  // (no vector load: see there)
 
   // One tile group.  The first call (the workgroup's own group; the host
   // gives every workgroup one group when they fit) is a copy of its own, so
@@ -530,7 +531,10 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     const u32x2_t sc = __builtin_amdgcn_raw_buffer_load_b64(srs, (uint32_t)(tt * kTileRows + 4 * q) * 2u, 0, 0);
     const uint16_t sc_last = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(srs, (uint32_t)(P.n - 1) * 2u, 0, 0);
 
-    if (w == (int)blockIdx.x) build_pair_table_lanes<KB>(table, cb_lane, tid, kLinThreads);
+    // (the codebook is read here, after the weight loads: read at entry, the
+    // wait for it came before the part's descriptor loads, one more round
+    // trip ahead of every weight load)
+    if (w == (int)blockIdx.x) build_pair_table_lanes<KB>(table, codebook_lane_scalar<KB>(codebook, lane), tid, kLinThreads);
     if (key != staged) {
       if (staged >= 0) __syncthreads();  // the previous group's reads of z and scr are done
       lin_stage_z<ROT, BIG, lin_pre(KB)>(a, P, xf, pre, pu0, npu, rnpu, zl, scr, tid, wave, lane);
