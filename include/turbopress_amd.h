@@ -182,6 +182,9 @@ int tp_tcq_gemv_tiled(const uint16_t* z, int64_t ldz, int64_t batch,
  * workgroup in LDS for the K range it streams, then the decode-GEMV, bias add
  * and fp16 output, in ONE kernel launch.  x: fp16 [batch, ldx] (ldx and d
  * multiples of 4, 8-byte aligned); other arguments as tp_tcq_gemv_tiled.
+ * At batch <= 8 a 4-byte aligned codebook takes the one-pass kernel (which
+ * reads it as dwords through the scalar cache); any other runs the earlier
+ * tiled kernels, with the same results.
  * Replaces turbopress/runtime.py:312-316 + 332-333 (fwht_scale, packed_gemv,
  * bias). */
 int tp_packed_linear_forward(const uint16_t* x, int64_t ldx, int64_t batch,

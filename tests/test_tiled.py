@@ -333,6 +333,41 @@ def test_packed_linear_forward_abi_batch_9_to_32(cuda, d, block, batch, x_offset
     assert int(ws.count_nonzero()) == 0  # split-K workspace back to zero
 
 
+@pytest.mark.parametrize("batch", [1, 4])
+def test_packed_linear_forward_abi_misaligned_codebook(cuda, batch):
+    """A codebook only 2-byte aligned: the one-pass kernel reads it as dwords
+    through the scalar cache and declines it, and the call runs the older
+    tiled kernels, with the same results (the aligned call beside it takes
+    the one-pass kernel)."""
+    from turbopress_amd import _lib
+    from turbopress_amd.runtime import PackedTCQLinear
+    n, d = 200, 2560
+    p = make_payload(n, d, 3, 64, seed=31 + batch)
+    lin = PackedTCQLinear(p, mode="hip")
+    x = make_activation(batch, d, seed=batch).to(cuda)
+    cb = lin.codebook
+    raw = torch.zeros(cb.numel() + 1, dtype=torch.float16, device=cuda)
+    cbs = raw[1: 1 + cb.numel()]
+    cbs.copy_(cb)
+    assert cbs.data_ptr() % 4 == 2
+    buf, pb = lin.tiled_packed, lin._tiled_geo["path_bytes"]
+    ws = hk.gemv_workspace(n, 32, cuda)
+    ys = []
+    for cbp in (cb.data_ptr(), cbs.data_ptr()):
+        y = torch.full((batch, n), float("nan"), dtype=torch.float16, device=cuda)
+        st = _lib.lib().tp_packed_linear_forward(
+            x.data_ptr(), d, batch, lin.rot_scale.data_ptr(), p["block"], buf.data_ptr(), buf.data_ptr() + pb,
+            lin.scales.data_ptr(), cbp, 0, n, d, 3, 64, y.data_ptr(), n,
+            ws.data_ptr(), ws.numel(), torch.cuda.current_stream(cuda).cuda_stream)
+        assert st == 0
+        ys.append(y)
+    torch.cuda.synchronize()
+    ref = O.tiled_forward(payload_numpy(p), x.cpu().numpy())
+    for y in ys:
+        assert O.max_rel(y.float().cpu().numpy(), ref) <= GEMV_TOL
+    assert int(ws.count_nonzero()) == 0
+
+
 def _random_case(seed):
     """A seeded (n, d, bits, n_states, batch): d with Hadamard blocks from 32
     to 2048 columns, n not a multiple of the 16-row tile, batch 1..32."""
