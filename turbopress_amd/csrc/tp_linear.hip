@@ -109,7 +109,7 @@ struct LinArgs {
   uint32_t r_pu, r_pu_last;  // lin_recip of a K part's units: every part but the last, the last (or only) part
   uint32_t r_batch;          // lin_recip(batch)
   int32_t sk, sk_last;       // chunks of c units in a K part: every part but the last, the last (or only) part
-  int32_t reserved;
+  float hrecip;              // fp32(1 / hdiv), correctly rounded
   LinPart part[kLinMaxParts];
   float* kws;                // K-split slices [kparts][T][16 rows][8] fp32 (zero between calls)
   uint32_t* kcnt;            // K-split arrival counter per row tile (zero between calls)
@@ -153,9 +153,8 @@ __device__ __forceinline__ void lin_chunk_stages(int hmax, int lane, float v[4])
 __device__ __forceinline__ void lin_chunk_fwht(const LinArgs& a, int lane, float v[4]) {
   if (a.hb >= kChunkCols) lin_chunk_stages<true>(kChunkCols, lane, v);
   else lin_chunk_stages<false>(a.hb, lane, v);
-  const float r = 1.f / a.hdiv;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = div_by_block_root(v[e], a.hdiv, r);
+  for (int e = 0; e < 4; ++e) v[e] = div_by_block_root_fx(v[e], a.hdiv, a.hrecip);
 }
 
 // z of one 256-column chunk of batch row b for Hadamard blocks <= 512, four
@@ -164,7 +163,14 @@ __device__ __forceinline__ void lin_chunk_fwht(const LinArgs& a, int lane, float
 // inside the chunk, then / sqrt(hb).  Columns past d are zero.
 __device__ void lin_rotate_chunk(const LinArgs& a, const LinPart& P, int b, int cs, int lane, float v[4]) {
   const uint16_t* xr = P.x + (size_t)b * P.ldx;
-  v[0] = v[1] = v[2] = v[3] = 0.f;
+  // v = 0 + (+-x rs) + ...: each product of two fp16 values is exact in fp32,
+  // so fma(x, +-rs, v) rounds as the add does (one v_fma_mix_f32 from the
+  // fp16 halves; the sign of a term is the sign bit of its rs halves).  The
+  // +0 start sits in an opaque register: a literal one lets the compiler
+  // split the first fma into converts and a product.
+  float pz = 0.f;
+  __asm__("" : "+v"(pz));
+  v[0] = v[1] = v[2] = v[3] = pz;
   // (hb is a power of two: masks and shifts)
   const int nsub = a.hb > kChunkCols ? a.hb >> 8 : 1;
   const int base = a.hb > kChunkCols ? cs & ~(a.hb - 1) : cs;
@@ -172,12 +178,13 @@ __device__ void lin_rotate_chunk(const LinArgs& a, const LinPart& P, int b, int 
   for (int i = 0; i < nsub; ++i) {
     const int c0 = base + i * kChunkCols + lane * 4;
     if (c0 < a.d) {  // d is a multiple of 4: a lane's group is wholly inside or outside
-      float xv[4], rv[4];
-      load4h(xr + c0, xv);
-      load4h(P.rs + c0, rv);
-      const bool neg = __popc(i & o) & 1;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] += neg ? -(xv[e] * rv[e]) : xv[e] * rv[e];
+      const uint2 xw = gld2(xr + c0), rw = gld2(P.rs + c0);
+      const uint32_t sgn = (__popc(i & o) & 1) ? 0x80008000u : 0u;
+      const uint32_t r0 = rw.x ^ sgn, r1 = rw.y ^ sgn;
+      v[0] = __builtin_fmaf(hlo(xw.x), hlo(r0), v[0]);
+      v[1] = __builtin_fmaf(hhi(xw.x), hhi(r0), v[1]);
+      v[2] = __builtin_fmaf(hlo(xw.y), hlo(r1), v[2]);
+      v[3] = __builtin_fmaf(hhi(xw.y), hhi(r1), v[3]);
     }
   }
   lin_chunk_fwht(a, lane, v);
@@ -243,18 +250,28 @@ __device__ __forceinline__ XPre<NPRE> lin_prefetch_x(const LinArgs& a, const Lin
 // x * rs of prefetched item k (the signed sum of both chunks of a 512-block).
 template <int NPRE>
 __device__ __forceinline__ void lin_pre_product(const LinArgs& a, const XPre<NPRE>& f, int k, int cs, float v[4]) {
-  float xv[4], rv[4];
-  unpack4h(uint2{f.x[k][0][0], f.x[k][0][1]}, xv);
-  unpack4h(uint2{f.r[k][0][0], f.r[k][0][1]}, rv);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = 0.f + xv[e] * rv[e];
+  // as lin_rotate_chunk: v = 0 + x rs (+- x' rs' of the block's other chunk),
+  // one v_fma_mix_f32 per term and column, the sign in the rs halves
+  float pz = 0.f;
+  __asm__("" : "+v"(pz));
+  float b[4] = {pz, pz, pz, pz};
   if (a.hb > kChunkCols && a.hb <= 2 * kChunkCols) {
-    const bool neg = (cs & (a.hb - 1)) != 0;  // second chunk of the block: row 1 of H_2
-    unpack4h(uint2{f.x[k][1][0], f.x[k][1][1]}, xv);
-    unpack4h(uint2{f.r[k][1][0], f.r[k][1][1]}, rv);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) v[e] += neg ? -(xv[e] * rv[e]) : xv[e] * rv[e];
+    // second chunk of the block: row 1 of H_2, the other chunk's term negated
+    const uint32_t sgn = (cs & (a.hb - 1)) != 0 ? 0x80008000u : 0u;
+    const uint32_t x0 = f.x[k][1][0], x1 = f.x[k][1][1];
+    const uint32_t r0 = f.r[k][1][0] ^ sgn, r1 = f.r[k][1][1] ^ sgn;
+    b[0] = __builtin_fmaf(hlo(x0), hlo(r0), pz);
+    b[1] = __builtin_fmaf(hhi(x0), hhi(r0), pz);
+    b[2] = __builtin_fmaf(hlo(x1), hlo(r1), pz);
+    b[3] = __builtin_fmaf(hhi(x1), hhi(r1), pz);
   }
+  // (p + (0 + b) here, (0 + p) + b before: equal for every sign of zero,
+  // and for nonzero terms both are the one rounding of an exact sum)
+  const uint32_t x0 = f.x[k][0][0], x1 = f.x[k][0][1], r0 = f.r[k][0][0], r1 = f.r[k][0][1];
+  v[0] = __builtin_fmaf(hlo(x0), hlo(r0), b[0]);
+  v[1] = __builtin_fmaf(hhi(x0), hhi(r0), b[1]);
+  v[2] = __builtin_fmaf(hlo(x1), hlo(r1), b[2]);
+  v[3] = __builtin_fmaf(hhi(x1), hhi(r1), b[3]);
 }
 
 __device__ __forceinline__ void store4h(uint16_t* p, const float v[4]) {
@@ -280,7 +297,7 @@ __device__ void lin_stage_big(const LinArgs& a, const LinPart& P, uint16_t* zl, 
   const int colw = 256 * wave + 4 * m;  // this thread's columns inside a tile
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(P.x, (uint32_t)((a.batch - 1) * P.ldx + a.d) * 2u);
   const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(P.rs, (uint32_t)a.d * 2u);
-  const float c = a.hdiv, r = 1.f / c;
+  const float c = a.hdiv, r = a.hrecip;
   // radix-4 step over wave bits s, s + 1 (column distances 256 << s and
   // 512 << s): u_k = the value of wave (w with those bits = k), then the
   // natural-order H_4 row of this wave's two bits (distance 256 << s first)
@@ -842,6 +859,7 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   a.tpw = (int32_t)best.tpw;
   a.zstride = (int32_t)zstride;
   a.hdiv = (float)__builtin_sqrt((double)hb);
+  a.hrecip = 1.f / a.hdiv;
   a.kparts = (int32_t)best.kparts;
   a.pu = (int32_t)best.pu;
   a.r_s = lin_recip(best.sc);
@@ -852,7 +870,6 @@ int linear_forward_fast(const TiledLinearArgs* ls, int n_lin, int64_t batch, con
   a.sk_last = (int32_t)((G4 - (best.kparts - 1) * best.pu + best.c - 1) / best.c);
   a.kws = nullptr;
   a.kcnt = nullptr;
-  a.reserved = 0;
   int64_t g0acc = 0;
   for (int i = 0; i < kLinMaxParts; ++i) {
     const TiledLinearArgs& l = ls[i < n_lin ? i : 0];
