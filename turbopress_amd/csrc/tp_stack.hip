@@ -1253,30 +1253,34 @@ __device__ __forceinline__ ZChunkN<2048 / NT> wide_load_z(__amdgpu_buffer_rsrc_t
   return c;
 }
 
+// (lcol: the lane's group of 8 columns -- the lane itself, or its
+// wide_rotate relabeling)
 template <int NT = kWideThreads>
-__device__ __forceinline__ void wide_store_z(uint16_t* zb, const ZChunkN<2048 / NT>& c, int batch, int tid) {
+__device__ __forceinline__ void wide_store_z(uint16_t* zb, const ZChunkN<2048 / NT>& c, int batch, int tid,
+                                             int lcol) {
 #pragma unroll
   for (int k = 0; k < 2048 / NT; ++k) {
     const int i = tid + NT * k;
-    const int row = i >> 6, c8 = (i & 63) * 8;
+    const int row = i >> 6, c8 = lcol * 8;
     if (row < batch) *reinterpret_cast<u32x4_t*>(zb + zl_index(row, c8)) = c.v[k];
   }
 }
 
 // ROT (per-linear launches at Hadamard blocks <= 512, every chunk then a
-// whole number of blocks): thread tid's two 8-column pieces of chunk ch of
-// the unrotated input and of rot_scale (columns past d read as zero).
+// whole number of blocks): thread tid's two 8-column pieces (columns
+// 8 lcol ..) of chunk ch of the unrotated input and of rot_scale (columns
+// past d read as zero).
 struct XChunk {
   u32x4_t x[2], r[2];
 };
-__device__ __forceinline__ XChunk wide_load_x(const LinearDesc& L, int batch, int ch, int tid) {
+__device__ __forceinline__ XChunk wide_load_x(const LinearDesc& L, int batch, int ch, int tid, int lcol) {
   const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(L.x, (uint32_t)(batch * L.ldx) * 2u);
   const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(L.rs, (uint32_t)L.d * 2u);
   XChunk c;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int i = tid + kWideThreads * k;
-    const int row = i >> 6, col = ch * kZCols + (i & 63) * 8;
+    const int row = i >> 6, col = ch * kZCols + lcol * 8;
     const bool in = row < batch && col < L.d;  // d % 8 == 0: a piece is wholly in or out
     c.x[k] = __builtin_amdgcn_raw_buffer_load_b128(xrs, in ? (uint32_t)(row * L.ldx + col) * 2u : kOutOfRange, 0, 0);
     c.r[k] = __builtin_amdgcn_raw_buffer_load_b128(rrs, in ? (uint32_t)col * 2u : kOutOfRange, 0, 0);
@@ -1284,24 +1288,41 @@ __device__ __forceinline__ XChunk wide_load_x(const LinearDesc& L, int batch, in
   return c;
 }
 
+// The lane's group of 8 columns in wide_rotate's pieces: the relabeling of
+// the tile transform (rot_lane_index), so that every lane stage below
+// distance 128 is one DPP move.
+__device__ __forceinline__ int wide_lane_col(int lane) { return rot_lane_index(lane); }
+
 // z = fp16(blockFWHT(x * rot_scale) / sqrt(hb)) of the pieces: a wave holds
-// one row's 512 columns (8 per lane), so the butterflies at distance 1..4
-// run in registers and 8..256 across lanes, in increasing distance as the
-// reference's transform, all in fp32, one rounding to fp16.
+// one row's 512 columns (8 per lane, columns 8 wide_lane_col ..), so the
+// butterflies at distance 1..4 run in registers and 8..256 across lanes, in
+// increasing distance as the reference's transform, all in fp32, one
+// rounding to fp16 -- the steps of the tile transform (tp_rotate_tile.h):
+// the products fused into the distance-1 stage as v_fma_mix_f32, each lane
+// stage one DPP move (bpermute at distance 128, 256) and one FMA.  (One
+// path for every block size, stages tested at run time: a second,
+// unrolled path for 512-column blocks pushed the kernel into scratch.)
+template <int K>
+__device__ __forceinline__ void wide_lane_stage(float* v, int m, int lane4, int hb) {
+  if ((8 << K) < hb) {
+    const float sg = __builtin_bit_cast(float, 0x3F800000u | (((uint32_t)m << (31 - K)) & 0x80000000u));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(sg, v[e], rot_partner<K>(v[e], lane4));
+  }
+}
 __device__ __forceinline__ ZChunk wide_rotate(const XChunk& c, int lane, int hb, float hdiv) {
   ZChunk z;
   const float rdiv = 1.f / hdiv;
+  const int m = rot_lane_index(lane), lane4 = 4 * lane;
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
+    const u32x2_t xw[2] = {u32x2_t{c.x[k][0], c.x[k][1]}, u32x2_t{c.x[k][2], c.x[k][3]}};
+    const u32x2_t rw[2] = {u32x2_t{c.r[k][0], c.r[k][1]}, u32x2_t{c.r[k][2], c.r[k][3]}};
     float v[8];
+    if (hb > 1) rot_products<true, 2>(xw, rw, v);  // with distance 1
+    else rot_products<false, 2>(xw, rw, v);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const uint32_t xw = c.x[k][e], rw = c.r[k][e];
-      v[2 * e] = h2f((uint16_t)xw) * h2f((uint16_t)rw);
-      v[2 * e + 1] = h2f((uint16_t)(xw >> 16)) * h2f((uint16_t)(rw >> 16));
-    }
-#pragma unroll
-    for (int h = 1; h < 8; h <<= 1) {
+    for (int h = 2; h < 8; h <<= 1) {  // distances 2, 4
       if (h < hb) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -1313,18 +1334,13 @@ __device__ __forceinline__ ZChunk wide_rotate(const XChunk& c, int lane, int hb,
         }
       }
     }
-    // (the upper lane of a pair keeps p - v: one FMA with the lane's sign)
-#pragma unroll
-    for (int sft = 0; sft < 6; ++sft) {
-      if ((8 << sft) < hb) {
-        const float sg = ((lane >> sft) & 1) ? -1.f : 1.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float p = sft < 4 ? lane_xor_row(v[e], 1 << sft) : __shfl_xor(v[e], 1 << sft, 64);
-          v[e] = __builtin_fmaf(sg, v[e], p);
-        }
-      }
-    }
+    wide_lane_stage<0>(v, m, lane4, hb);  // distance 8
+    wide_lane_stage<1>(v, m, lane4, hb);
+    wide_lane_stage<2>(v, m, lane4, hb);
+    wide_lane_stage<3>(v, m, lane4, hb);
+    wide_lane_stage<4>(v, m, lane4, hb);
+    wide_lane_stage<5>(v, m, lane4, hb);  // distance 256
+    // (the corrected reciprocal is exact for a power-of-two root as well)
 #pragma unroll
     for (int e = 0; e < 4; ++e)
       z.v[k][e] = pack_h2(div_by_block_root(v[2 * e], hdiv, rdiv), div_by_block_root(v[2 * e + 1], hdiv, rdiv));
@@ -1510,14 +1526,15 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
   // table build).
   ZChunkN<2048 / NT> c0;
   XChunk x0;
-  if constexpr (ROT) x0 = wide_load_x(L, batch, ch0, tid);
+  const int lcol = ROT ? wide_lane_col(lane) : lane;  // the lane's z columns in a chunk
+  if constexpr (ROT) x0 = wide_load_x(L, batch, ch0, tid, lcol);
   else c0 = wide_load_z<NT>(zrs, zld, batch, ch0, tid);
   ChunkRegs<MW> ra[TPW];
 #pragma unroll
   for (int k = 0; k < TPW; ++k) ra[k] = load_chunk<MW>(L, pt[k], mt[k], ch0, q, r);
   if (build_table) build_pair_table_lanes<KB>(table, cb_lane, tid, NT);
   if constexpr (ROT) c0 = wide_rotate(x0, lane, L.hb, L.hdiv);
-  wide_store_z<NT>(zl + (ch0 & 1) * kWideChunkHalves, c0, batch, tid);
+  wide_store_z<NT>(zl + (ch0 & 1) * kWideChunkHalves, c0, batch, tid, lcol);
   __syncthreads();
   // Chunk ch: prefetch chunk ch + 1 of z, decode + multiply ch, store the
   // prefetch into the other buffer, one barrier (the next chunk's buffer is
@@ -1527,7 +1544,7 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
     ZChunkN<2048 / NT> nx;
     XChunk nxx;
     if (more) {
-      if constexpr (ROT) nxx = wide_load_x(L, batch, ch + 1, tid);
+      if constexpr (ROT) nxx = wide_load_x(L, batch, ch + 1, tid, lcol);
       else nx = wide_load_z<NT>(zrs, zld, batch, ch + 1, tid);
     }
     const uint16_t* zb = zl + (ch & 1) * kWideChunkHalves;
@@ -1555,7 +1572,7 @@ __device__ void wide_block(const LinearDesc& L, int wb, int ch0, int ch1, const 
     }
     if (more) {
       if constexpr (ROT) nx = wide_rotate(nxx, lane, L.hb, L.hdiv);
-      wide_store_z<NT>(zl + ((ch + 1) & 1) * kWideChunkHalves, nx, batch, tid);
+      wide_store_z<NT>(zl + ((ch + 1) & 1) * kWideChunkHalves, nx, batch, tid, lcol);
     }
     __syncthreads();
   };
