@@ -289,8 +289,9 @@ __device__ __forceinline__ void store4h(uint16_t* p, const float v[4]) {
 // waves as radix-4 steps through `scr` (w bits 0, 1, then 2, 3) -- every
 // butterfly the reference's, in its order, so z is the reference's bit for
 // bit (and the same z as the stack rotation's).
-template <int LOGH>
-__device__ void lin_stage_big(const LinArgs& a, const LinPart& P, uint16_t* zl, float* scr, int wave, int lane) {
+template <int LOGH, int NPRE>
+__device__ void lin_stage_big(const LinArgs& a, const LinPart& P, const XPre<NPRE>& f, bool pre, uint16_t* zl,
+                              float* scr, int wave, int lane) {
   static_assert(LOGH >= 10 && LOGH <= 12, "blocks of 1024 .. 4096 columns");
   const int tpr = (a.d + kRotTile - 1) / kRotTile;  // tiles per batch row
   const int m = rot_lane_index(lane), lane4 = 4 * lane;
@@ -318,13 +319,10 @@ __device__ void lin_stage_big(const LinArgs& a, const LinPart& P, uint16_t* zl, 
       v[e] = __builtin_fmaf(s2, s23, s01);
     }
   };
-  for (int it = 0; it < a.batch * tpr; ++it) {
-    int tcol = 0;
-    const int b = udiv_small(it, tpr, &tcol);  // (it < batch * tpr)
+  // One tile: batch row b, tile tcol, this thread's words xw, rw.
+  auto tile = [&](int b, int tcol, const u32x2_t xw, const u32x2_t rw) __attribute__((always_inline)) {
     const int col = tcol * kRotTile + colw;
     const bool ok = col < a.d;
-    const u32x2_t xw = load4h_words(xrs, ok ? (uint32_t)(b * P.ldx + col) : kOutOfRange / 2u);
-    const u32x2_t rw = load4h_words(rrs, ok ? (uint32_t)col : kOutOfRange / 2u);
     float v[4];
     rot_products<true, 1>(&xw, &rw, v);
     rot_reg_stage<2, 2, LOGH, 4>(v);
@@ -347,7 +345,38 @@ __device__ void lin_stage_big(const LinArgs& a, const LinPart& P, uint16_t* zl, 
       radix4(v, 2);  // distances 1024, 2048
     }
     if (ok) *reinterpret_cast<u32x2_t*>(zl + b * a.zstride + col) = rot_z4<LOGH>(v, c, r);
+  };
+  // The first tile from the words lin_prefetch_big loaded ahead of the
+  // weights (a copy of its own: inside the loop, the wait before the tile's
+  // words would also cover every weight load), then the rest.
+  int it0 = 0;
+  if (pre) {
+    tile(0, 0, f.x[0][0], f.r[0][0]);
+    it0 = 1;
   }
+  for (int it = it0; it < a.batch * tpr; ++it) {
+    int tcol = 0;
+    const int b = udiv_small(it, tpr, &tcol);  // (it < batch * tpr)
+    const int col = tcol * kRotTile + colw;
+    const bool ok = col < a.d;
+    tile(b, tcol, load4h_words(xrs, ok ? (uint32_t)(b * P.ldx + col) : kOutOfRange / 2u),
+         load4h_words(rrs, ok ? (uint32_t)col : kOutOfRange / 2u));
+  }
+}
+
+// BIG: this thread's words of the first tile (batch row 0, columns
+// 256 w + 4 m(l) ..), loaded before the weights so that staging it waits for
+// them only.
+template <int NPRE>
+__device__ __forceinline__ XPre<NPRE> lin_prefetch_big(const LinArgs& a, const LinPart& P, int wave, int lane) {
+  XPre<NPRE> f;
+  const __amdgpu_buffer_rsrc_t xrs = buffer_rsrc(P.x, (uint32_t)((a.batch - 1) * P.ldx + a.d) * 2u);
+  const __amdgpu_buffer_rsrc_t rrs = buffer_rsrc(P.rs, (uint32_t)a.d * 2u);
+  const int col = 256 * wave + 4 * rot_lane_index(lane);
+  const bool ok = col < a.d;
+  f.x[0][0] = load4h_words(xrs, ok ? (uint32_t)col : kOutOfRange / 2u);
+  f.r[0][0] = load4h_words(rrs, ok ? (uint32_t)col : kOutOfRange / 2u);
+  return f;
 }
 
 // Stage z rows [0, batch) x columns [pu0 * 256, (pu0 + npu) * 256) of linear
@@ -399,9 +428,9 @@ __device__ void lin_stage_z(const LinArgs& a, const LinPart& P, const XPre<NPRE>
     return;
   } else {
     const int logh = __builtin_ctz((unsigned)a.hb);  // 10, 11 or 12 (uniform)
-    if (logh == 10) lin_stage_big<10>(a, P, zl, scr, wave, lane);
-    else if (logh == 11) lin_stage_big<11>(a, P, zl, scr, wave, lane);
-    else lin_stage_big<12>(a, P, zl, scr, wave, lane);
+    if (logh == 10) lin_stage_big<10>(a, P, f, pre, zl, scr, wave, lane);
+    else if (logh == 11) lin_stage_big<11>(a, P, f, pre, zl, scr, wave, lane);
+    else lin_stage_big<12>(a, P, f, pre, zl, scr, wave, lane);
   }
 }
 
@@ -515,6 +544,8 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
     XPre<lin_pre(KB)> xf;
     if constexpr (ROT && !BIG) {
       if (pre) xf = lin_prefetch_x<lin_pre(KB)>(a, P, pu0, npu, rnpu, wave, lane);
+    } else if constexpr (ROT && BIG) {
+      if (pre) xf = lin_prefetch_big<lin_pre(KB)>(a, P, wave, lane);
     }
 
     // Every weight load of this wave, then the halo word (path word 1 of
