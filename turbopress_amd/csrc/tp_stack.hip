@@ -602,11 +602,13 @@ __device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1
       // Halo: word 1 of the previous segment comes from the lane 16 below
       // (K block q-1); lanes of K block 0 take the previous unit's last
       // segment (from lanes of K block 3, carried in x1_last); zero at a
-      // row start.
-      const uint32_t provide = (E.q == 3) ? (pgu == 0 ? 0u : x1_last) : R[k].X[1];
+      // row start (x1_last is cleared at every block end, not tested per
+      // unit).
+      const uint32_t provide = (E.q == 3) ? x1_last : R[k].X[1];
       slot_unit<KB, NS, SB, MW, NZ>(R[k], provide, E.lane, E.laneoff, E.table, acc);
       x1_last = R[k].X[1];
       if (++pgu == cur.G4) {
+        x1_last = 0u;  // (the next block starts a row)
         // Block end: accumulator `slot` holds this lane's valid column; sum
         // the slots of each batch row, lanes of slot 0 write rows 4q..4q+3.
         const TP_CONST LinearDesc& L = cread(E.P.lin + cur.li);
