@@ -621,19 +621,33 @@ __device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1
 #pragma unroll
           for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(acc[s][i], m, v[i]);
         }
-#pragma unroll
-        for (int w = SB; w < 16; w <<= 1)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], w, 64);
+        row_sum_from<SB>(v);  // (slot-0 lanes: the xor butterfly's sums)
+        // (the sums stay ahead of the store branch, where each DPP move folds
+        // into its add; sunk into the branch, the moves stayed outside)
+        __asm__ volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
         if (cur.t < L.T && E.slot == 0 && E.bb < E.batch) {
           const int row0 = cur.t * kTileRows + 4 * E.q;
+          uint16_t* yr = L.y + (size_t)E.bb * L.ldy + row0;
+          // Rows 4q..4q+3 in one 8-byte store when all four exist, there is
+          // no bias and y's rows are 8-byte aligned (the same values as the
+          // row-by-row stores; one address instead of four).
+          const bool quad = !L.bias && ((reinterpret_cast<uintptr_t>(L.y) | ((uintptr_t)L.ldy << 1)) & 7u) == 0;
+          if (quad && row0 + 4 <= L.n) {
+            u32x2_t o;
+            o.x = (uint32_t)f2h(v[0] * h2f((uint16_t)sc.v[0])) |
+                  ((uint32_t)f2h(v[1] * h2f((uint16_t)sc.v[1])) << 16);
+            o.y = (uint32_t)f2h(v[2] * h2f((uint16_t)sc.v[2])) |
+                  ((uint32_t)f2h(v[3] * h2f((uint16_t)sc.v[3])) << 16);
+            *(TP_GLOBAL u32x2_t*)yr = o;
+          } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int row = row0 + i;
-            if (row >= L.n) continue;
-            uint16_t out = f2h(v[i] * h2f((uint16_t)sc.v[i]));
-            if (L.bias) out = f2h(h2f(out) + h2f(gld(L.bias + row)));
-            gst(L.y + (size_t)E.bb * L.ldy + row, out);
+            for (int i = 0; i < 4; ++i) {
+              const int row = row0 + i;
+              if (row >= L.n) continue;
+              uint16_t out = f2h(v[i] * h2f((uint16_t)sc.v[i]));
+              if (L.bias) out = f2h(h2f(out) + h2f(gld(L.bias + row)));
+              gst(yr + i, out);
+            }
           }
         }
 #pragma unroll
@@ -1020,10 +1034,7 @@ __device__ __forceinline__ void ord_flush(float4_t* acc, float4_t* dst, uint32_t
     for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(acc[k][i], msk, v[i]);
     acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
   }
-#pragma unroll
-  for (int w = SB; w < 16; w <<= 1)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], w, 64);
+  row_sum_from<SB>(v);  // (slot-0 lanes: the xor butterfly's sums)
   if (slot == 0) dst[pl] = v;
 }
 

@@ -114,6 +114,26 @@ __device__ __forceinline__ float lane_xor_row(float v, int m) {
   return __builtin_bit_cast(float, y);
 }
 
+// x plus lane l + W of the same row of 16 lanes (DPP row_ror:16-W, no LDS).
+// Steps W = S, 2S, .., 8 leave in lane l the sum of lanes l, l + S, ..
+// (mod 16) of its row; for lanes l < S the additions are those of the
+// lane-xor butterfly (v += shfl_xor(v, W) for the same W), in the same
+// order, so their sums are bit-identical to it.
+template <int W>
+__device__ __forceinline__ float add_row_rot(float x) {
+  static_assert(W >= 1 && W <= 8, "row rotation");
+  const int y = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x120 | (16 - W), 0xF, 0xF, true);
+  return x + __builtin_bit_cast(float, y);
+}
+template <int W, typename V>
+__device__ __forceinline__ void row_sum_from(V& v) {
+  if constexpr (W < 16) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = add_row_rot<W>(v[i]);
+    row_sum_from<2 * W>(v);
+  }
+}
+
 // Delay mask of a window-coordinate generator: bit t set when the subset bit
 // XORs in the path bit t columns back.
 __host__ __device__ constexpr uint32_t delay_mask(uint32_t g, int m) {
