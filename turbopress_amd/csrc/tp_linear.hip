@@ -615,10 +615,7 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
 #pragma unroll
         for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(acc[s][i], msk, v[i]);
       }
-#pragma unroll
-      for (int w = SB; w < 16; w <<= 1)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] += __shfl_xor(v[i], w, 64);
+      row_sum_from<SB>(v);  // (slot-0 lanes: the xor butterfly's sums)
       *reinterpret_cast<float4_t*>(scr + (wave * 64 + lane) * 4) = v;
     }
     __syncthreads();
