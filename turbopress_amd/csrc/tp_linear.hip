@@ -142,8 +142,9 @@ __device__ __forceinline__ void lin_chunk_stages(int hmax, int lane, float v[4])
       const float sg = ((lane >> sft) & 1) ? -1.f : 1.f;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float p = sft < 4 ? lane_xor_row(v[e], 1 << sft) : __shfl_xor(v[e], 1 << sft, 64);
-        v[e] = __builtin_fmaf(sg, v[e], p);
+        if (sft == 4) v[e] = lane_swap_butterfly<4>(v[e], sg);
+        else if (sft == 5) v[e] = lane_swap_butterfly<5>(v[e], sg);
+        else v[e] = __builtin_fmaf(sg, v[e], lane_xor_row(v[e], 1 << sft));
       }
     }
   }

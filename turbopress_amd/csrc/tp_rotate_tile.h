@@ -16,7 +16,7 @@
 // one radix-4 step through LDS (the wave).  m(l) puts lanes so that the
 // partner of m bits 0..3 is one DPP move: lane xor 1 / 2 / 7 / 8 (two quad
 // permutes, the half-row mirror, a row rotation by 8); bits 4 and 5 are
-// lane xor 16 and 32 (bpermute).  Stages are unrolled per block size
+// lane xor 16 and 32 (one permlane swap each).  Stages are unrolled per block size
 // (template LOGH = log2 hb), so that no stage is skipped at run time.
 #pragma once
 #include "tp_slot.h"
@@ -59,7 +59,10 @@ __device__ __forceinline__ void rot_lane_stage(float* v, int m, int lane4) {
     // +-1.0: the sign bit from bit K of m
     const float sg = __builtin_bit_cast(float, 0x3F800000u | (((uint32_t)m << (31 - K)) & 0x80000000u));
 #pragma unroll
-    for (int e = 0; e < N; ++e) v[e] = __builtin_fmaf(sg, v[e], rot_partner<K>(v[e], lane4));
+    for (int e = 0; e < N; ++e) {
+      if constexpr (K >= 4) v[e] = lane_swap_butterfly<K>(v[e], sg);  // (m bits 4, 5 are lane bits 4, 5)
+      else v[e] = __builtin_fmaf(sg, v[e], rot_partner<K>(v[e], lane4));
+    }
   }
 }
 

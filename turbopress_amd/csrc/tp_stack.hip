@@ -1312,7 +1312,9 @@ __device__ __forceinline__ int wide_lane_col(int lane) { return rot_lane_index(l
 // increasing distance as the reference's transform, all in fp32, one
 // rounding to fp16 -- the steps of the tile transform (tp_rotate_tile.h):
 // the products fused into the distance-1 stage as v_fma_mix_f32, each lane
-// stage one DPP move (bpermute at distance 128, 256) and one FMA.  (One
+// stage one DPP move (bpermute at distance 128, 256: a permlane swap there,
+// which writes both of its registers, pushed this kernel into scratch) and
+// one FMA.  (One
 // path for every block size, stages tested at run time: a second,
 // unrolled path for 512-column blocks pushed the kernel into scratch.)
 template <int K>

@@ -134,6 +134,30 @@ __device__ __forceinline__ void row_sum_from(V& v) {
   }
 }
 
+// One butterfly at lane distance 16 (K = 4) or 32 (K = 5) without LDS:
+// v_permlane16_swap / v_permlane32_swap with both operands v leave the
+// lower lane's value in r[0] and the upper lane's in r[1], in both lanes of
+// each pair (16-lane rows 0-1 and 2-3 / the two 32-lane halves), so
+// fma(sg, r[1], r[0]) is own + partner in the lower lane (sg = +1) and
+// partner - own in the upper one (sg = -1): the same sum or difference of
+// the same two values as fma(sg, own, partner) with a bpermute partner.
+template <int K>
+__device__ __forceinline__ float lane_swap_butterfly(float v, float sg) {
+  static_assert(K == 4 || K == 5, "lane distance 16 or 32");
+  const uint32_t x = __builtin_bit_cast(uint32_t, v);
+  uint32_t lo, hi;
+  if constexpr (K == 4) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    lo = r[0];
+    hi = r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    lo = r[0];
+    hi = r[1];
+  }
+  return __builtin_fmaf(sg, __builtin_bit_cast(float, hi), __builtin_bit_cast(float, lo));
+}
+
 // Delay mask of a window-coordinate generator: bit t set when the subset bit
 // XORs in the path bit t columns back.
 __host__ __device__ constexpr uint32_t delay_mask(uint32_t g, int m) {
