@@ -489,7 +489,6 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 15, q = lane >> 4;
   const int slot = r / SB, bb = r % SB;
-  const uint32_t slot_bit = 1u << slot;
   const uint32_t laneoff = lane_offsets<KB>(lane);
   const uint32_t pv = (uint32_t)(q * kTileRows + r) * 8u;
   const uint32_t mv = (uint32_t)(q * kTileRows + r) * MW * 4u;
@@ -608,15 +607,9 @@ __global__ void __launch_bounds__(kLinThreads) tcq_linear_kernel(const LinArgs a
           prev = R[u].X[1];
         }
       }
-      // accumulator `slot` holds this lane's column; sum the slots of each batch row
-      float4_t v = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < SLOTS; ++s) {
-        const float msk = (float)__builtin_amdgcn_ubfe(slot_bit, (uint32_t)s, 1u);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(acc[s][i], msk, v[i]);
-      }
-      row_sum_from<SB>(v);  // (slot-0 lanes: the xor butterfly's sums)
+      // accumulator `slot` holds this lane's column; the slot-0 lanes' sums
+      // over the slots of each batch row (the other lanes' values are unused)
+      const float4_t v = slot_column_sums<SLOTS, SB>(acc);
       *reinterpret_cast<float4_t*>(scr + (wave * 64 + lane) * 4) = v;
     }
     __syncthreads();

@@ -435,7 +435,7 @@ struct SlotEnv {
   __amdgpu_buffer_rsrc_t zrs;   // the whole z buffer
   int total, batch, wave, lane, q, slot, bb, ordered, spin_limit, tid;
   uint32_t tbase;  // blocks [0, tbase) are assigned by workgroup index, the rest by ticket
-  uint32_t laneoff, pv, mv, slot_bit;
+  uint32_t laneoff, pv, mv;
 };
 
 // A block of the stream as one wave sees it (wave-uniform).
@@ -612,16 +612,8 @@ __device__ __forceinline__ void slot_stream(const SlotEnv& E, int blk0, int blk1
         // Block end: accumulator `slot` holds this lane's valid column; sum
         // the slots of each batch row, lanes of slot 0 write rows 4q..4q+3.
         const TP_CONST LinearDesc& L = cread(E.P.lin + cur.li);
-        // v = acc[slot], as a masked sum (per-slot lane compares would stay
-        // live in scalar registers across the loop)
-        float4_t v = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < SLOTS; ++s) {
-          const float m = (float)__builtin_amdgcn_ubfe(E.slot_bit, (uint32_t)s, 1u);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(acc[s][i], m, v[i]);
-        }
-        row_sum_from<SB>(v);  // (slot-0 lanes: the xor butterfly's sums)
+        // the slot-0 lanes' column sums (DPP adds across the row)
+        float4_t v = slot_column_sums<SLOTS, SB>(acc);
         // (the sums stay ahead of the store branch, where each DPP move folds
         // into its add; sunk into the branch, the moves stayed outside)
         __asm__ volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
@@ -756,7 +748,6 @@ tcq_stack_slot_kernel(const char* __restrict__ plan_ro, char* __restrict__ plan_
   E.q = E.lane >> 4;
   E.slot = r / SB;
   E.bb = r % SB;
-  E.slot_bit = 1u << E.slot;
   E.laneoff = lane_offsets<KB>(E.lane);
   E.pv = (uint32_t)(E.q * kTileRows + r) * 8u;        // path byte offset in a unit
   E.mv = (uint32_t)(E.q * kTileRows + r) * MW * 4u;   // member byte offset in a unit
@@ -1025,16 +1016,10 @@ __device__ __forceinline__ void ord_zv(uint32_t* zv, const OrdDesc& D, int q, in
 // lane's column; the slots of each batch row are summed and the 16 (K
 // block, batch row) sums land in the slot-0 lanes.
 template <int SLOTS, int SB>
-__device__ __forceinline__ void ord_flush(float4_t* acc, float4_t* dst, uint32_t slot_bit, int slot, int pl) {
-  float4_t v = float4_t{0.f, 0.f, 0.f, 0.f};
+__device__ __forceinline__ void ord_flush(float4_t* acc, float4_t* dst, int slot, int pl) {
+  const float4_t v = slot_column_sums<SLOTS, SB>(acc);  // (valid in the slot-0 lanes)
 #pragma unroll
-  for (int k = 0; k < SLOTS; ++k) {
-    const float msk = (float)__builtin_amdgcn_ubfe(slot_bit, (uint32_t)k, 1u);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(acc[k][i], msk, v[i]);
-    acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
-  }
-  row_sum_from<SB>(v);  // (slot-0 lanes: the xor butterfly's sums)
+  for (int k = 0; k < SLOTS; ++k) acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
   if (slot == 0) dst[pl] = v;
 }
 
@@ -1066,7 +1051,6 @@ tcq_stack_ordered_kernel(const char* __restrict__ plan_ro, char* __restrict__ pl
   const int r = lane & 15, q = lane >> 4;
   const int slot = r / SB, bb = r % SB;
   const int pl = q * 4 + bb;  // this lane's (K block, batch row) sum in the slot-0 lanes
-  const uint32_t slot_bit = 1u << slot;
   const uint32_t laneoff = lane_offsets<KB>(lane);
   const uint32_t pv = (uint32_t)(q * kTileRows + r) * 8u;
   const uint32_t mv = (uint32_t)(q * kTileRows + r) * MW * 4u;
@@ -1114,7 +1098,7 @@ tcq_stack_ordered_kernel(const char* __restrict__ plan_ro, char* __restrict__ pl
           slot_unit<KB, NS, SB, MW, NZ>(B.R[u], provide, lane, laneoff, table, acc);
           prev = B.R[u].X[1];
           kd = ord_next_k(kd, D.G4);
-          if (kd == 0) ord_flush<SLOTS, SB>(acc, part[wave][td++ % kOrdSegs], slot_bit, slot, pl);
+          if (kd == 0) ord_flush<SLOTS, SB>(acc, part[wave][td++ % kOrdSegs], slot, pl);
         }
         if (more) {
           ord_unit<MW, NZ>(B.R[u], D, D.c0 + base + UMAX + u, kl, pv, mv, zv, zrs);
@@ -1122,7 +1106,7 @@ tcq_stack_ordered_kernel(const char* __restrict__ plan_ro, char* __restrict__ pl
         }
       }
     }
-    if (D.nu > 0 && kd != 0) ord_flush<SLOTS, SB>(acc, part[wave][td % kOrdSegs], slot_bit, slot, pl);
+    if (D.nu > 0 && kd != 0) ord_flush<SLOTS, SB>(acc, part[wave][td % kOrdSegs], slot, pl);
     // Every load of the block has been consumed or was out of range (those
     // return at once): an explicit wait tells the compiler so, and keeps its
     // own waits out of the y stores and the next block's loads below.

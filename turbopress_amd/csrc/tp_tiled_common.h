@@ -114,24 +114,39 @@ __device__ __forceinline__ float lane_xor_row(float v, int m) {
   return __builtin_bit_cast(float, y);
 }
 
-// x plus lane l + W of the same row of 16 lanes (DPP row_ror:16-W, no LDS).
-// Steps W = S, 2S, .., 8 leave in lane l the sum of lanes l, l + S, ..
-// (mod 16) of its row; for lanes l < S the additions are those of the
-// lane-xor butterfly (v += shfl_xor(v, W) for the same W), in the same
-// order, so their sums are bit-identical to it.
+// a plus the b of lane l + W of the same row of 16 lanes (DPP row_ror:16-W).
 template <int W>
-__device__ __forceinline__ float add_row_rot(float x) {
+__device__ __forceinline__ float add_rot(float a, float b) {
   static_assert(W >= 1 && W <= 8, "row rotation");
-  const int y = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), 0x120 | (16 - W), 0xF, 0xF, true);
-  return x + __builtin_bit_cast(float, y);
+  const int y = __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, b), 0x120 | (16 - W), 0xF, 0xF, true);
+  return a + __builtin_bit_cast(float, y);
 }
-template <int W, typename V>
-__device__ __forceinline__ void row_sum_from(V& v) {
-  if constexpr (W < 16) {
+template <int N, int W>
+__device__ __forceinline__ void slot_pair_levels(float4_t* t) {
+  if constexpr (N > 1) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = add_row_rot<W>(v[i]);
-    row_sum_from<2 * W>(v);
+    for (int j = 0; j < N / 2; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[j][i] = add_rot<W>(t[2 * j][i], t[2 * j + 1][i]);
+    slot_pair_levels<N / 2, 2 * W>(t);
   }
+}
+// Column sums of the slot accumulators (SLOTS = 16 / SB, the lane of row
+// position r holding its valid column in acc[r / SB]) for the lanes of slot
+// 0: lane l (l % 16 < SB) gets acc[0] of lane l + acc[1] of lane l + SB +
+// .. + acc[SLOTS-1] of lane l + (SLOTS-1) SB, added pairwise (adjacent
+// slots, then adjacent pairs, ..).  That is the order of the masked form --
+// acc[slot] per lane, then v += lane v xor SB, 2 SB, .. -- so the sums of
+// finite values are bit-identical to it, with (SLOTS - 1) x 4 DPP adds
+// instead of SLOTS x 4 masked FMAs and then (log2 SLOTS) x 4 adds.
+template <int SLOTS, int SB>
+__device__ __forceinline__ float4_t slot_column_sums(const float4_t* acc) {
+  static_assert(SLOTS * SB == 16, "16 columns per row");
+  float4_t t[SLOTS];
+#pragma unroll
+  for (int s = 0; s < SLOTS; ++s) t[s] = acc[s];
+  slot_pair_levels<SLOTS, SB>(t);
+  return t[0];
 }
 
 // One butterfly at lane distance 16 (K = 4) or 32 (K = 5) without LDS:
