@@ -135,10 +135,10 @@ __device__ __forceinline__ void slot_pair_levels(float4_t* t) {
 // position r holding its valid column in acc[r / SB]) for the lanes of slot
 // 0: lane l (l % 16 < SB) gets acc[0] of lane l + acc[1] of lane l + SB +
 // .. + acc[SLOTS-1] of lane l + (SLOTS-1) SB, added pairwise (adjacent
-// slots, then adjacent pairs, ..).  That is the order of the masked form --
-// acc[slot] per lane, then v += lane v xor SB, 2 SB, .. -- so the sums of
-// finite values are bit-identical to it, with (SLOTS - 1) x 4 DPP adds
-// instead of SLOTS x 4 masked FMAs and then (log2 SLOTS) x 4 adds.
+// slots, then adjacent pairs, ..).  Selecting acc[slot] in every lane and
+// then adding lane v xor SB, 2 SB, .. (a butterfly) adds the same values in
+// the same order, so for finite values the sums are bit-identical to that
+// form, here with (SLOTS - 1) x 4 DPP adds and no selection.
 template <int SLOTS, int SB>
 __device__ __forceinline__ float4_t slot_column_sums(const float4_t* acc) {
   static_assert(SLOTS * SB == 16, "16 columns per row");
