@@ -137,6 +137,53 @@ def test_stack_split_launches_match_run(cuda, batch):
     assert stack.error() == 0
 
 
+@pytest.mark.parametrize("shapes", ["mixed", "ragged"])
+@pytest.mark.parametrize("ordered", [False, True])
+@pytest.mark.parametrize("batch", [1, 3, 4])
+def test_stack_unaligned_output_rows(cuda, shapes, ordered, batch):
+    """Outputs through the C ABI at an odd element offset with an odd row
+    stride: a lane's four rows are not 8-byte aligned there, so the slot
+    kernel stores them one by one instead of in one 8-byte store.  Same bits
+    as the plan with aligned outputs, and nothing written outside the rows."""
+    import ctypes
+
+    from turbopress_amd import _lib
+    from turbopress_amd import hip_kernel as hk
+    shape_list = MIXED if shapes == "mixed" else RAGGED
+    payloads, stack = _build(cuda, shape_list, batch, ordered=ordered)
+    stack.run()
+    torch.cuda.synchronize()
+    ref = [o.clone() for o in stack.outputs]
+    arr = (_lib.StackLinear * len(stack.linears))()
+    bufs, lds = [], []
+    for i, (lin, x, ph) in enumerate(zip(stack.linears, stack.inputs, stack.phases)):
+        ldy = lin.out_features + 3
+        buf = torch.full((batch * ldy + 1,), float("nan"), dtype=torch.float16, device=cuda)
+        bufs.append(buf)
+        lds.append(ldy)
+        pb = lin._tiled_geo["path_bytes"]
+        arr[i] = _lib.StackLinear(
+            lin.tiled_packed.data_ptr(), lin.tiled_packed.data_ptr() + pb, x.data_ptr(), lin.in_features,
+            lin.rot_scale.data_ptr(), lin.block, lin.scales.data_ptr(), 0, buf.data_ptr() + 2, ldy,
+            lin.out_features, lin.in_features, ph, 0)
+    lib = _lib.lib()
+    nbytes = int(lib.tp_stack_plan_bytes(arr, len(stack.linears), stack.bits, batch))
+    plan = torch.zeros(nbytes, dtype=torch.uint8, device=cuda)
+    torch.cuda.synchronize()
+    _lib.check(lib.tp_stack_plan_init(arr, len(stack.linears), stack.bits, batch, plan.data_ptr(), nbytes),
+               "stack_plan_init")
+    _lib.check(lib.tp_stack_run(plan.data_ptr(), batch, stack.codebook.data_ptr(), stack.bits, stack.n_states,
+                                int(ordered), stack.total_blocks, hk.current_stream_ptr(cuda)), "stack_run")
+    torch.cuda.synchronize()
+    for lin, buf, ldy, r in zip(stack.linears, bufs, lds, ref):
+        rows = buf[1:].view(batch, ldy)
+        assert torch.equal(rows[:, :lin.out_features].view(torch.int16), r.view(torch.int16))
+        assert torch.isnan(rows[:, lin.out_features:]).all() and torch.isnan(buf[0])
+    err = ctypes.c_int()
+    _lib.check(lib.tp_stack_error(plan.data_ptr(), ctypes.byref(err)), "stack_error")
+    assert err.value == 0
+
+
 def test_stack_rejects_mixed_codebooks(cuda):
     from turbopress_amd.decode_step import LinearStack
     from turbopress_amd.runtime import PackedTCQLinear
