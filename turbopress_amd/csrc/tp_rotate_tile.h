@@ -16,7 +16,8 @@
 // one radix-4 step through LDS (the wave).  m(l) puts lanes so that the
 // partner of m bits 0..3 is one DPP move: lane xor 1 / 2 / 7 / 8 (two quad
 // permutes, the half-row mirror, a row rotation by 8); bits 4 and 5 are
-// lane xor 16 and 32 (one permlane swap each).  Stages are unrolled per block size
+// lane xor 16 and 32 (a permlane swap or a bpermute each, see
+// rot_lane_stage).  Stages are unrolled per block size
 // (template LOGH = log2 hb), so that no stage is skipped at run time.
 #pragma once
 #include "tp_slot.h"
@@ -53,14 +54,18 @@ __device__ __forceinline__ float rot_partner(float v, int lane4) {
 // block: the lane whose m has bit K set keeps partner - own, the other
 // own + partner, each one FMA fma(+-1, own, partner) (the product is exact,
 // so the sum rounds as the add or subtract does).
-template <int K, int LOGH, int N = kRotEPT>
+//
+// SWAP: distances 16 and 32 lanes by permlane swaps (VALU, no LDS: shorter
+// latency, for launches that are one latency chain), else by bpermute (an
+// LDS instruction beside one VALU FMA: for launches bound by VALU issue).
+template <int K, int LOGH, int N = kRotEPT, bool SWAP = true>
 __device__ __forceinline__ void rot_lane_stage(float* v, int m, int lane4) {
   if constexpr ((4 << K) < (1 << LOGH)) {
     // +-1.0: the sign bit from bit K of m
     const float sg = __builtin_bit_cast(float, 0x3F800000u | (((uint32_t)m << (31 - K)) & 0x80000000u));
 #pragma unroll
     for (int e = 0; e < N; ++e) {
-      if constexpr (K >= 4) v[e] = lane_swap_butterfly<K>(v[e], sg);  // (m bits 4, 5 are lane bits 4, 5)
+      if constexpr (K >= 4 && SWAP) v[e] = lane_swap_butterfly<K>(v[e], sg);  // (m bits 4, 5 are lane bits 4, 5)
       else v[e] = __builtin_fmaf(sg, v[e], rot_partner<K>(v[e], lane4));
     }
   }
@@ -121,15 +126,15 @@ __device__ __forceinline__ void rot_products(const u32x2_t* xw, const u32x2_t* r
 // The stages of a block of 2^LOGH columns (at most 4096) from distance 2
 // (rot_products ran the first) to 512, unnormalized: registers and lanes
 // only.
-template <int LOGH>
+template <int LOGH, bool SWAP = true>
 __device__ __forceinline__ void rot_stages_lanes(float v[kRotEPT], int m, int lane4) {
   rot_reg_stage<2, 2, LOGH>(v);
-  rot_lane_stage<0, LOGH>(v, m, lane4);
-  rot_lane_stage<1, LOGH>(v, m, lane4);
-  rot_lane_stage<2, LOGH>(v, m, lane4);
-  rot_lane_stage<3, LOGH>(v, m, lane4);
-  rot_lane_stage<4, LOGH>(v, m, lane4);
-  rot_lane_stage<5, LOGH>(v, m, lane4);
+  rot_lane_stage<0, LOGH, kRotEPT, SWAP>(v, m, lane4);
+  rot_lane_stage<1, LOGH, kRotEPT, SWAP>(v, m, lane4);
+  rot_lane_stage<2, LOGH, kRotEPT, SWAP>(v, m, lane4);
+  rot_lane_stage<3, LOGH, kRotEPT, SWAP>(v, m, lane4);
+  rot_lane_stage<4, LOGH, kRotEPT, SWAP>(v, m, lane4);
+  rot_lane_stage<5, LOGH, kRotEPT, SWAP>(v, m, lane4);
   rot_reg_stage<4, 256, LOGH>(v);
   rot_reg_stage<8, 512, LOGH>(v);
 }
@@ -170,9 +175,9 @@ __device__ __forceinline__ void rot_stage_waves(float v[kRotEPT], int w, int m, 
 
 // Every stage of a block of 2^LOGH columns (at most 4096) from distance 2,
 // all 256 threads of the workgroup on one tile.
-template <int LOGH>
+template <int LOGH, bool SWAP = true>
 __device__ __forceinline__ void rot_stages(float v[kRotEPT], int w, int m, int lane4, float* ex) {
-  rot_stages_lanes<LOGH>(v, m, lane4);
+  rot_stages_lanes<LOGH, SWAP>(v, m, lane4);
   if constexpr ((1 << LOGH) > 1024) rot_stage_waves<LOGH>(v, w, m, ex, true);
 }
 

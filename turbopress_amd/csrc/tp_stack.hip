@@ -258,7 +258,7 @@ __host__ __device__ inline int64_t rot_tiles(int64_t batch, int64_t d, int64_t h
 }
 
 // One packed tile: load x * rot_scale, transform, divide, store z.
-template <int LOGH>
+template <int LOGH, bool SWAP>
 __device__ __forceinline__ void rot_packed_tile(const TP_CONST RotItem& L, int w, int m, int lane4, float* ex) {
   constexpr int HB = 1 << LOGH;
   const uint32_t nblk = (uint32_t)L.nblk, nbt = (uint32_t)L.nbt, ldx = (uint32_t)L.ldx;
@@ -306,7 +306,7 @@ __device__ __forceinline__ void rot_packed_tile(const TP_CONST RotItem& L, int w
   }
   float v[kRotEPT];
   rot_products<(LOGH > 0)>(xw, rw, v);
-  rot_stages<LOGH>(v, w, m, lane4, ex);
+  rot_stages<LOGH, SWAP>(v, w, m, lane4, ex);
   const float c = L.hdiv, r = L.hrecip;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
@@ -318,8 +318,9 @@ __device__ __forceinline__ void rot_packed_tile(const TP_CONST RotItem& L, int w
 // Packed tiles (items [0, n_rot_packed) of the plan), one workgroup per
 // tile when the host knows the tile count (ONE_TILE: the descriptor is the
 // first load, the x / rot_scale loads the second); otherwise a grid-stride
-// loop bounded by the plan's count.
-template <bool ONE_TILE>
+// loop bounded by the plan's count.  SWAP: see rot_lane_stage (the host
+// takes it for launches of at most a few tiles per CU).
+template <bool ONE_TILE, bool SWAP>
 __global__ void __launch_bounds__(kRotThreads)
 tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
   __shared__ float ex[kRotTile];
@@ -337,19 +338,19 @@ tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
                      "s"(L.ldx), "s"(L.nblk), "s"(L.nbt), "s"(L.logh), "s"(L.hrecip)
                      : "memory");
     switch (L.logh) {  // (uniform)
-      case 0: rot_packed_tile<0>(L, w, m, lane4, ex); break;
-      case 1: rot_packed_tile<1>(L, w, m, lane4, ex); break;
-      case 2: rot_packed_tile<2>(L, w, m, lane4, ex); break;
-      case 3: rot_packed_tile<3>(L, w, m, lane4, ex); break;
-      case 4: rot_packed_tile<4>(L, w, m, lane4, ex); break;
-      case 5: rot_packed_tile<5>(L, w, m, lane4, ex); break;
-      case 6: rot_packed_tile<6>(L, w, m, lane4, ex); break;
-      case 7: rot_packed_tile<7>(L, w, m, lane4, ex); break;
-      case 8: rot_packed_tile<8>(L, w, m, lane4, ex); break;
-      case 9: rot_packed_tile<9>(L, w, m, lane4, ex); break;
-      case 10: rot_packed_tile<10>(L, w, m, lane4, ex); break;
-      case 11: rot_packed_tile<11>(L, w, m, lane4, ex); break;
-      case 12: rot_packed_tile<12>(L, w, m, lane4, ex); break;
+      case 0: rot_packed_tile<0, SWAP>(L, w, m, lane4, ex); break;
+      case 1: rot_packed_tile<1, SWAP>(L, w, m, lane4, ex); break;
+      case 2: rot_packed_tile<2, SWAP>(L, w, m, lane4, ex); break;
+      case 3: rot_packed_tile<3, SWAP>(L, w, m, lane4, ex); break;
+      case 4: rot_packed_tile<4, SWAP>(L, w, m, lane4, ex); break;
+      case 5: rot_packed_tile<5, SWAP>(L, w, m, lane4, ex); break;
+      case 6: rot_packed_tile<6, SWAP>(L, w, m, lane4, ex); break;
+      case 7: rot_packed_tile<7, SWAP>(L, w, m, lane4, ex); break;
+      case 8: rot_packed_tile<8, SWAP>(L, w, m, lane4, ex); break;
+      case 9: rot_packed_tile<9, SWAP>(L, w, m, lane4, ex); break;
+      case 10: rot_packed_tile<10, SWAP>(L, w, m, lane4, ex); break;
+      case 11: rot_packed_tile<11, SWAP>(L, w, m, lane4, ex); break;
+      case 12: rot_packed_tile<12, SWAP>(L, w, m, lane4, ex); break;
       default: break;
     }
   }
@@ -360,7 +361,7 @@ tcq_stack_rotate_kernel(const char* __restrict__ plan_ro) {
 // 4096-column sub-tile of the block through distances 1..2048, then
 // distance 4096 (sub-tile pairs) and 8192 (pairs of pairs); sub-tile o of
 // the result takes the signs of row o.
-template <bool ONE_TILE>
+template <bool ONE_TILE, bool SWAP>
 __global__ void __launch_bounds__(kRotThreads)
 tcq_stack_rotate_big_kernel(const char* __restrict__ plan_ro) {
   __shared__ float ex[kRotTile];
@@ -395,7 +396,7 @@ tcq_stack_rotate_big_kernel(const char* __restrict__ plan_ro) {
       }
       float t[kRotEPT];
       rot_products<true>(xw, rw, t);
-      rot_stages<kRotMaxLogH>(t, w, m, lane4, ex);
+      rot_stages<kRotMaxLogH, SWAP>(t, w, m, lane4, ex);
       if ((i & 1) == 0) {
 #pragma unroll
         for (int e = 0; e < kRotEPT; ++e) a[e] = t[e];
@@ -2079,14 +2080,26 @@ extern "C" int tp_stack_rotate(void* plan, int64_t batch, void* stream) {
   const bool known = plan_lookup(plan, &reg);
   hipStream_t s = (hipStream_t)stream;
   if (known) {
-    if (reg.n_rot_packed > 0)
-      hipLaunchKernelGGL((tcq_stack_rotate_kernel<true>), dim3(reg.n_rot_packed), dim3(kRotThreads), 0, s, ro);
-    if (reg.n_rot_big > 0)
-      hipLaunchKernelGGL((tcq_stack_rotate_big_kernel<true>), dim3(reg.n_rot_big), dim3(kRotThreads), 0, s, ro);
+    // a few tiles per CU: one latency chain, the permlane butterflies; more
+    // (batch 32: 7488 tiles at Qwen3-4B): VALU issue, the bpermute ones
+    // (batch-32 step 510.1 -> 508.8 us against the permlane ones)
+    const bool swap = (int64_t)reg.n_rot_packed + reg.n_rot_big <= 4 * (int64_t)device_cu_count();
+    if (reg.n_rot_packed > 0) {
+      if (swap)
+        hipLaunchKernelGGL((tcq_stack_rotate_kernel<true, true>), dim3(reg.n_rot_packed), dim3(kRotThreads), 0, s, ro);
+      else
+        hipLaunchKernelGGL((tcq_stack_rotate_kernel<true, false>), dim3(reg.n_rot_packed), dim3(kRotThreads), 0, s, ro);
+    }
+    if (reg.n_rot_big > 0) {
+      if (swap)
+        hipLaunchKernelGGL((tcq_stack_rotate_big_kernel<true, true>), dim3(reg.n_rot_big), dim3(kRotThreads), 0, s, ro);
+      else
+        hipLaunchKernelGGL((tcq_stack_rotate_big_kernel<true, false>), dim3(reg.n_rot_big), dim3(kRotThreads), 0, s, ro);
+    }
   } else {
     const int grid = 2 * device_cu_count();
-    hipLaunchKernelGGL((tcq_stack_rotate_kernel<false>), dim3(grid), dim3(kRotThreads), 0, s, ro);
-    hipLaunchKernelGGL((tcq_stack_rotate_big_kernel<false>), dim3(grid), dim3(kRotThreads), 0, s, ro);
+    hipLaunchKernelGGL((tcq_stack_rotate_kernel<false, false>), dim3(grid), dim3(kRotThreads), 0, s, ro);
+    hipLaunchKernelGGL((tcq_stack_rotate_big_kernel<false, false>), dim3(grid), dim3(kRotThreads), 0, s, ro);
   }
   return launch_status();
 }
