@@ -277,9 +277,25 @@ def test_stack_rotation_bit_exact(cuda, batch):
     rows into 4096-column tiles (d = 12, block 4: one tile holds every row;
     d = 2560 at batch 3: a tile of 8 blocks spans rows 0 and 1, the last
     tile is partial); larger blocks run per row."""
+    _rotation_bit_exact(cuda, batch, ROT_DS)
+
+
+ROT_DS = [12, 40, 96, 128, 576, 1024, 2048, 2560, 3072, 4096, 6144, 8192, 9728, 16384]
+
+
+def test_stack_rotation_bit_exact_many_tiles(cuda):
+    """The same at batch 32 with every width three times: more than four
+    4096-column tiles per CU, where the launch takes its bpermute butterflies
+    at lane distance 16 / 32 (the permlane swaps below that)."""
+    ds = ROT_DS * 3
+    tiles = sum(-(-32 * d // 4096) if d <= 4096 or d % 4096 else 32 * d // 4096 for d in ds)
+    assert tiles > 4 * torch.cuda.get_device_properties(cuda).multi_processor_count
+    _rotation_bit_exact(cuda, 32, ds)
+
+
+def _rotation_bit_exact(cuda, batch, ds):
     from turbopress_amd.decode_step import LinearStack
     from turbopress_amd.runtime import PackedTCQLinear
-    ds = [12, 40, 96, 128, 576, 1024, 2048, 2560, 3072, 4096, 6144, 8192, 9728, 16384]
     payloads, entries = [], []
     for i, d in enumerate(ds):
         p = make_payload(16, d, 3, 64, seed=400 + i)
